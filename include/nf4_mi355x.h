@@ -1,0 +1,161 @@
+/*
+ * nf4_mi355x.h - C ABI of the MI355X (gfx950) NF4 quantized-linear library.
+ *
+ * The library dequantizes bitsandbytes-layout NF4 weights and multiplies with them, forward and
+ * backward, on one AMD Instinct MI355X.  Every entry point takes plain device pointers, sizes, a
+ * dtype code and a HIP stream (as void*), launches asynchronously on that stream and returns an
+ * int status (NF4_OK == 0).  The caller allocates every output and workspace; the library owns
+ * no device memory and keeps no state between calls, so it is reentrant and thread-safe.
+ *
+ * Weight format (bitsandbytes 0.50.2 QuantState, as read by the reference at
+ * /root/reference/solution/nf4.py:46-53,112-131):
+ *   packed   uint8 [ceil(rows*cols/2)]: element i of the row-major weight in byte i/2,
+ *            high nibble for even i (nf4.py:33-35);
+ *   absmax   per block of `blocksize` elements: uint8 codes when nested (double quant),
+ *            fp32 otherwise;
+ *   absmax2  fp32 [ceil(nblocks/blocksize2)] and code2 fp32[256] (nested only);
+ *   offset   fp32 mean added after the 8-bit dequant (nested only);
+ *   code     fp32[16], the NF4 table.
+ * Dequantized element: round(code[nib] * (fp32(code2[q] * absmax2[b / blocksize2]) + offset))
+ * with every product/sum rounded separately in fp32 and one round-to-nearest-even at the end.
+ */
+#ifndef NF4_MI355X_H
+#define NF4_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NF4_ABI_VERSION 1
+
+/* status codes */
+#define NF4_OK 0
+#define NF4_ERR_ARG 1          /* null pointer, negative size, bad dtype, misaligned pointer */
+#define NF4_ERR_UNSUPPORTED 2  /* a layout or shape this library does not cover */
+#define NF4_ERR_LAUNCH 3       /* the HIP runtime reported an error */
+#define NF4_ERR_WORKSPACE 4    /* the workspace passed is smaller than required */
+
+/* dtype codes: activations, outputs and (for dequant) the dequantized weight */
+#define NF4_F16 0
+#define NF4_BF16 1
+#define NF4_F32 2
+
+/* One NF4 weight [rows, cols] (out_features x in_features) in bitsandbytes layout. */
+typedef struct nf4_weight {
+    const uint8_t *packed;
+    const void *absmax;    /* uint8 [nblocks] if nested else fp32 [nblocks] */
+    const float *absmax2;  /* nested: fp32 [ceil(nblocks / blocksize2)], else NULL */
+    const float *code2;    /* nested: fp32 [256], else NULL */
+    const float *code;     /* fp32 [16] */
+    float offset;          /* nested: the mean offset, else 0 */
+    int32_t nested;
+    int64_t rows;
+    int64_t cols;
+    int32_t blocksize;
+    int32_t blocksize2;
+} nf4_weight;
+
+/* A rank-r LoRA adapter on output segment `seg` of a stacked projection (peft semantics,
+ * y_seg += scale * drop(x) @ A^T @ B^T; reference layer.py:875-878, 1072-1090).
+ * Forward reads t and b; the input-gradient GEMM reads a and da. */
+typedef struct nf4_lora {
+    int32_t seg;
+    int32_t rank;          /* 1..16 */
+    float scale;           /* alpha / r */
+    const void *t;         /* [M, rank] drop(x) @ A^T, GEMM dtype (forward) */
+    const void *b;         /* [rows_seg, rank] LoRA B, GEMM dtype (forward) */
+    const void *a;         /* [rank, K] LoRA A, GEMM dtype (input gradient) */
+    const void *da;        /* [M, rank] scale * dY_seg @ B, GEMM dtype (input gradient) */
+} nf4_lora;
+
+/* Library version / status text. */
+int nf4_abi_version(void);
+const char *nf4_status_string(int status);
+
+/* ---------------------------------------------------------------- standalone dequantization */
+
+/* out[rows, cols] = dequant(w) in out_dtype (F16, BF16 or F32).
+ * Replaces: dequantize_nf4(packed, quant_state, dtype) -> nf4_dequant_kernel
+ *           (/root/reference/solution/nf4.py:26-38, 69-77), with the absmax rebuild of
+ *           _absmax_fp32 (nf4.py:41-55) folded into the kernel. */
+int nf4_dequant(const nf4_weight *w, void *out, int out_dtype, void *stream);
+
+/* Up to NF4_MAX_SEGMENTS weights with equal cols, dequantized one after the other into one
+ * stacked [sum(rows), cols] buffer (q|k|v or gate|up).
+ * Replaces: _dequant(layers, dtype) -> nf4_dequant_multi_kernel
+ *           (/root/reference/solution/layer.py:45-73, 463-493). */
+#define NF4_MAX_SEGMENTS 8
+int nf4_dequant_multi(const nf4_weight *ws, int nw, void *out, int out_dtype, void *stream);
+
+/* ------------------------------------------------------------------ fused dequant-GEMMs */
+
+/* Y[M, sum(rows)] = X[M, K] @ W_stack^T (+ bias) (+ sum over loras scale * T @ B^T on the
+ * lora's segment columns), W dequantized inside the GEMM main loop, fp32 accumulation, one
+ * rounding to dtype (F16 or BF16).  X rows are ldx elements apart, Y rows ldy.
+ * Replaces: F.linear(x, dequantize_nf4(W), bias) in NF4Linear.forward (nf4.py:84-91); the
+ *           addmm / mm projection GEMMs of FusedDecoderLayer.forward with the LoRA terms
+ *           (layer.py:871-878, 893, 914, 929); RecomputedMLP's forward GEMMs (mlp.py:47-54).
+ * workspace may be NULL when nf4_linear_fwd_workspace() returns 0 for the same arguments. */
+int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx,
+                   const nf4_weight *ws, int nw, const void *bias,
+                   const nf4_lora *loras, int nlora,
+                   void *y, int64_t ldy, int dtype,
+                   void *workspace, size_t workspace_bytes, void *stream);
+size_t nf4_linear_fwd_workspace(int64_t m, const nf4_weight *ws, int nw, int dtype);
+
+/* dX[M, K] (+)= dY[M, sum(rows)] @ W_stack (+ sum over loras da @ A), the transposed
+ * dequant-GEMM.  accumulate != 0 adds into dX.
+ * Replaces: torch.matmul(grad, dequantize_nf4(W)) in NF4Linear.backward (nf4.py:93-99); the
+ *           input-gradient GEMMs of FusedDecoderLayer.backward (layer.py:1015, 1024-1032, 1061,
+ *           1086-1088) and RecomputedMLP.backward (mlp.py:65, 72-73). */
+int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy,
+                  const nf4_weight *ws, int nw,
+                  const nf4_lora *loras, int nlora,
+                  void *dx, int64_t lddx, int accumulate, int dtype,
+                  void *workspace, size_t workspace_bytes, void *stream);
+size_t nf4_linear_dx_workspace(int64_t m, const nf4_weight *ws, int nw, int dtype);
+
+/* ---------------------------------------------------------------------- LoRA side GEMMs */
+
+/* t[M, rank] = xd[M, K] @ A[rank, K]^T  (LoRA down-projection; layer.py:875, 877). */
+int nf4_lora_xa(const void *xd, int64_t m, int64_t k, int64_t ldx, const void *a, int rank,
+                void *t, int dtype, void *stream);
+
+/* da[M, rank] = scale * dY[M, N] @ B[N, rank]  (layer.py:1074-1078). */
+int nf4_lora_da(const void *dy, int64_t m, int64_t n, int64_t lddy, const void *b, int rank,
+                float scale, void *da, int dtype, void *stream);
+
+/* out = scale * U[M, P]^T @ V[M, rank], fp32, reduced over M (the LoRA weight gradients):
+ * transpose_out == 0 -> out[P, rank] (dB = s * dY^T @ T, layer.py:1075-1076);
+ * transpose_out != 0 -> out[rank, P] (dA = da^T @ xd, layer.py:1080-1081).
+ * workspace: nf4_lora_wgrad_workspace() bytes for the split-M partial sums. */
+int nf4_lora_wgrad(const void *u, int64_t m, int64_t p, int64_t ldu, const void *v, int rank,
+                   float scale, float *out, int transpose_out, int dtype,
+                   void *workspace, size_t workspace_bytes, void *stream);
+size_t nf4_lora_wgrad_workspace(int64_t m, int64_t p, int rank);
+
+/* -------------------------------------------------------------------------- small helpers */
+
+/* out[rows, cols] = silu(gate) * up, and its gradient (the SwiGLU step between the gate/up and
+ * down GEMMs of RecomputedMLP, mlp.py:26-39, 52, 70; example kernels swiglu.py:15-37).
+ * gate/up (and dgate/dup) rows are ld_gu elements apart, so they can be the two halves of the
+ * stacked gate|up GEMM output; out / grad rows are ld_h apart. */
+int nf4_swiglu_fwd(const void *gate, const void *up, int64_t ld_gu, void *out, int64_t ld_h,
+                   int64_t rows, int64_t cols, int dtype, void *stream);
+int nf4_swiglu_bwd(const void *grad, int64_t ld_h, const void *gate, const void *up,
+                   int64_t ld_gu, void *dgate, void *dup, int64_t rows, int64_t cols, int dtype,
+                   void *stream);
+
+/* out[N] = sum over rows of dY[M, N] (fp32): the bias gradient of NF4Linear.backward
+ * (nf4.py:100-101). */
+int nf4_bias_grad(const void *dy, int64_t m, int64_t n, int64_t lddy, float *out, int dtype,
+                  void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NF4_MI355X_H */

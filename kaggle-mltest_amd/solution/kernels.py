@@ -1,0 +1,192 @@
+"""Tensor-level wrappers of the C ABI: allocate outputs and workspaces with torch (device
+memory and streams only), pass raw pointers, launch on torch's current stream, raise on a
+nonzero status.  No arithmetic happens here."""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import DTYPE_CODE, NF4Lora, check, load, stream_of
+from .quant_state import weight_array, weight_desc
+
+GEMM_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def _code(dtype: torch.dtype, allowed=GEMM_DTYPES) -> int:
+    if dtype not in allowed:
+        raise TypeError(f"dtype {dtype} is not supported here (expected one of {allowed})")
+    return DTYPE_CODE[dtype]
+
+
+def _descs(weights):
+    """[(packed, quant_state), ...] -> ctypes array of descriptors."""
+    return weight_array([weight_desc(p, qs) for p, qs in weights])
+
+
+def _check_device(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("the NF4 kernels run on the GPU: every tensor must be on a cuda device")
+
+
+def dequant(weights, dtype=torch.float16, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Stacked [sum rows, cols] dequantized weight(s) (nf4_dequant_multi)."""
+    packed0 = weights[0][0]
+    _check_device(packed0)
+    rows = sum(int(qs.shape[0]) for _, qs in weights)
+    cols = int(weights[0][1].shape[1])
+    if out is None:
+        out = torch.empty((rows, cols), dtype=dtype, device=packed0.device)
+    arr = _descs(weights)
+    st = load().nf4_dequant_multi(arr, len(weights), out.data_ptr(),
+                                  _code(dtype, (torch.float16, torch.bfloat16, torch.float32)),
+                                  stream_of(out))
+    check(st, "nf4_dequant_multi")
+    return out
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def _lora_array(loras):
+    if not loras:
+        return None, 0
+    arr = (NF4Lora * len(loras))(*loras)
+    return arr, len(loras)
+
+
+def linear_fwd(x: torch.Tensor, weights, bias: torch.Tensor | None = None, loras=(),
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Y[M, sum rows] = x[M, K] @ W_stack^T (+ bias) (+ LoRA terms).  `loras`: NF4Lora structs
+    whose pointers stay alive for the call (the caller keeps the tensors)."""
+    _check_device(x, bias)
+    dt = _code(x.dtype)
+    m, k = x.shape
+    n = sum(int(qs.shape[0]) for _, qs in weights)
+    if out is None:
+        out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    arr = _descs(weights)
+    lib = load()
+    ws_bytes = lib.nf4_linear_fwd_workspace(m, arr, len(weights), dt)
+    ws = _workspace(ws_bytes, x.device)
+    larr, nl = _lora_array(loras)
+    st = lib.nf4_linear_fwd(x.data_ptr() if m else None, m, x.stride(0), arr, len(weights),
+                            bias.data_ptr() if bias is not None else None, larr, nl,
+                            out.data_ptr(), out.stride(0), dt,
+                            ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(x))
+    check(st, "nf4_linear_fwd")
+    return out
+
+
+def linear_dx(dy: torch.Tensor, weights, loras=(), out: torch.Tensor | None = None,
+              accumulate: bool = False) -> torch.Tensor:
+    """dX[M, K] (+)= dY[M, sum rows] @ W_stack (+ LoRA terms)."""
+    _check_device(dy)
+    dt = _code(dy.dtype)
+    m = dy.shape[0]
+    k = int(weights[0][1].shape[1])
+    if out is None:
+        out = torch.empty((m, k), dtype=dy.dtype, device=dy.device)
+        accumulate = False
+    arr = _descs(weights)
+    lib = load()
+    ws_bytes = lib.nf4_linear_dx_workspace(m, arr, len(weights), dt)
+    ws = _workspace(ws_bytes, dy.device)
+    larr, nl = _lora_array(loras)
+    st = lib.nf4_linear_dx(dy.data_ptr() if m else None, m, dy.stride(0), arr, len(weights),
+                           larr, nl, out.data_ptr(), out.stride(0), int(accumulate), dt,
+                           ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(dy))
+    check(st, "nf4_linear_dx")
+    return out
+
+
+def lora_xa(xd: torch.Tensor, a: torch.Tensor) -> torch.Tensor:
+    """t[M, r] = xd[M, K] @ A[r, K]^T."""
+    _check_device(xd, a)
+    m, k = xd.shape
+    r = a.shape[0]
+    t = torch.empty((m, r), dtype=xd.dtype, device=xd.device)
+    st = load().nf4_lora_xa(xd.data_ptr(), m, k, xd.stride(0), a.data_ptr(), r, t.data_ptr(),
+                            _code(xd.dtype), stream_of(xd))
+    check(st, "nf4_lora_xa")
+    return t
+
+
+def lora_da(dy: torch.Tensor, b: torch.Tensor, scale: float) -> torch.Tensor:
+    """da[M, r] = scale * dY[M, N] @ B[N, r]  (dY may be a column slice: rows stride(0) apart)."""
+    _check_device(dy, b)
+    m, n = dy.shape
+    r = b.shape[1]
+    da = torch.empty((m, r), dtype=dy.dtype, device=dy.device)
+    st = load().nf4_lora_da(dy.data_ptr(), m, n, dy.stride(0), b.data_ptr(), r, float(scale),
+                            da.data_ptr(), _code(dy.dtype), stream_of(dy))
+    check(st, "nf4_lora_da")
+    return da
+
+
+def lora_wgrad(u: torch.Tensor, v: torch.Tensor, scale: float, transpose_out: bool) -> torch.Tensor:
+    """scale * U[M, P]^T @ V[M, r] in fp32: [P, r], or [r, P] when transpose_out."""
+    _check_device(u, v)
+    m, p = u.shape
+    r = v.shape[1]
+    out = torch.empty((r, p) if transpose_out else (p, r), dtype=torch.float32, device=u.device)
+    lib = load()
+    ws_bytes = lib.nf4_lora_wgrad_workspace(m, p, r)
+    ws = _workspace(ws_bytes, u.device)
+    st = lib.nf4_lora_wgrad(u.data_ptr() if m else None, m, p, u.stride(0),
+                            v.data_ptr() if m else None, r, float(scale), out.data_ptr(),
+                            int(transpose_out), _code(u.dtype),
+                            ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(u))
+    check(st, "nf4_lora_wgrad")
+    return out
+
+
+def swiglu_fwd(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up for two [M, I] views with equal row stride (e.g. halves of gate|up)."""
+    _check_device(gate, up)
+    rows, cols = gate.shape
+    if up.stride(0) != gate.stride(0) or gate.stride(1) != 1 or up.stride(1) != 1:
+        raise ValueError("gate and up must be row-contiguous views with one row stride")
+    out = torch.empty((rows, cols), dtype=gate.dtype, device=gate.device)
+    st = load().nf4_swiglu_fwd(gate.data_ptr(), up.data_ptr(), gate.stride(0), out.data_ptr(),
+                               out.stride(0), rows, cols, _code(gate.dtype), stream_of(gate))
+    check(st, "nf4_swiglu_fwd")
+    return out
+
+
+def swiglu_bwd(grad: torch.Tensor, gate: torch.Tensor, up: torch.Tensor,
+               dgate: torch.Tensor, dup: torch.Tensor) -> None:
+    """dgate, dup (row-strided like gate/up; may be gate/up themselves) from grad [M, I]."""
+    _check_device(grad, gate, up)
+    rows, cols = gate.shape
+    st = load().nf4_swiglu_bwd(grad.data_ptr(), grad.stride(0), gate.data_ptr(), up.data_ptr(),
+                               gate.stride(0), dgate.data_ptr(), dup.data_ptr(), rows, cols,
+                               _code(gate.dtype), stream_of(gate))
+    check(st, "nf4_swiglu_bwd")
+
+
+def bias_grad(dy: torch.Tensor) -> torch.Tensor:
+    """Column sums of dY [M, N] in fp32."""
+    _check_device(dy)
+    m, n = dy.shape
+    out = torch.empty(n, dtype=torch.float32, device=dy.device)
+    st = load().nf4_bias_grad(dy.data_ptr() if m else None, m, n, dy.stride(0), out.data_ptr(),
+                              _code(dy.dtype), stream_of(dy))
+    check(st, "nf4_bias_grad")
+    return out
+
+
+def make_lora(seg: int, rank: int, scale: float, t=None, b=None, a=None, da=None) -> NF4Lora:
+    return NF4Lora(seg=seg, rank=rank, scale=float(scale),
+                   t=t.data_ptr() if t is not None else None,
+                   b=b.data_ptr() if b is not None else None,
+                   a=a.data_ptr() if a is not None else None,
+                   da=da.data_ptr() if da is not None else None)
+
+
+__all__ = ["dequant", "linear_fwd", "linear_dx", "lora_xa", "lora_da", "lora_wgrad",
+           "swiglu_fwd", "swiglu_bwd", "bias_grad", "make_lora", "GEMM_DTYPES", "_lib"]

@@ -1,0 +1,100 @@
+"""Qwen2 MLP that keeps only its input for the backward pass and recomputes gate|up there,
+on the HIP kernels.  Mirror of /root/reference/solution/mlp.py (`RecomputedMLP`, 42-74, same
+apply() signature; `patch_qwen2_mlp_recompute`, 123-157).
+
+gate and up run as ONE stacked dequant-GEMM launch ([M, 2I] output), the SwiGLU step reads its
+two halves in place, and the input gradient dgate W_gate + dup W_up is ONE transposed
+dequant-GEMM over the stacked pair, summed in fp32 (the reference adds two fp16 products).
+The reference's recompute budget (mlp.py:92-120) is a 15 GB-GPU memory policy and is not
+mirrored: this MLP always recomputes.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+from .quant_state import nf4_state_ok
+
+
+class RecomputedMLP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, gate_w, gate_qs, up_w, up_qs, down_w, down_qs):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        if x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        gate_w, up_w, down_w = gate_w.reshape(-1), up_w.reshape(-1), down_w.reshape(-1)
+        inter = int(gate_qs.shape[0])
+        gu = kernels.linear_fwd(x2, [(gate_w, gate_qs), (up_w, up_qs)])
+        hidden = kernels.swiglu_fwd(gu[:, :inter], gu[:, inter:])
+        del gu
+        out = kernels.linear_fwd(hidden, [(down_w, down_qs)])
+        ctx.save_for_backward(x2, gate_w, up_w, down_w)
+        ctx.qs, ctx.shape = (gate_qs, up_qs, down_qs), shape
+        return out.view(*shape[:-1], out.shape[-1])
+
+    @staticmethod
+    def backward(ctx, grad):
+        x2, gate_w, up_w, down_w = ctx.saved_tensors
+        gate_qs, up_qs, down_qs = ctx.qs
+        inter = int(gate_qs.shape[0])
+        grad = grad.reshape(-1, grad.shape[-1]).to(x2.dtype)
+        if grad.stride(0) % 8 or grad.data_ptr() % 16:
+            grad = grad.contiguous()
+        d_hidden = kernels.linear_dx(grad, [(down_w, down_qs)])
+        gu = kernels.linear_fwd(x2, [(gate_w, gate_qs), (up_w, up_qs)])
+        # the gradient of gate|up overwrites gate|up (each element is read, then written)
+        kernels.swiglu_bwd(d_hidden, gu[:, :inter], gu[:, inter:], gu[:, :inter], gu[:, inter:])
+        del d_hidden
+        dx = kernels.linear_dx(gu, [(gate_w, gate_qs), (up_w, up_qs)])
+        return dx.view(ctx.shape), None, None, None, None, None, None
+
+
+def _usable(layer, in_features):
+    """A frozen bias-free NF4 bitsandbytes layer (mlp.py:77-89)."""
+    from bitsandbytes.nn import Linear4bit
+
+    if type(layer) is not Linear4bit or layer.bias is not None or layer.weight.requires_grad:
+        return False
+    qs = getattr(layer.weight, "quant_state", None)
+    return nf4_state_ok(layer.weight, qs, in_features) and int(qs.blocksize) % 64 == 0 and \
+        int(qs.shape[1]) % int(qs.blocksize) == 0
+
+
+def patch_qwen2_mlp_recompute():
+    """Qwen2MLP.forward through RecomputedMLP under fp16 autocast (mlp.py:123-157).  Needs
+    bitsandbytes (the layers it serves are Linear4bit); raises ImportError without it."""
+    import bitsandbytes  # noqa: F401 - the layers this patch serves are bitsandbytes layers
+    from transformers.models.qwen2 import modeling_qwen2
+
+    cls = modeling_qwen2.Qwen2MLP
+    if getattr(cls.forward, "_nf4_recompute", False):
+        return
+    previous = cls.forward
+
+    def forward(self, x):
+        if not x.is_cuda or not torch.is_autocast_enabled("cuda") or \
+                torch.get_autocast_dtype("cuda") not in kernels.GEMM_DTYPES or \
+                getattr(getattr(self, "config", None), "hidden_act", "silu") != "silu" or \
+                not torch.is_grad_enabled() or \
+                x.dtype not in (torch.float16, torch.bfloat16, torch.float32) or x.numel() == 0:
+            return previous(self, x)
+        if not _usable(self.gate_proj, x.shape[-1]) or not _usable(self.up_proj, x.shape[-1]) or \
+                not _usable(self.down_proj, self.gate_proj.out_features):
+            return previous(self, x)
+        dtype = torch.get_autocast_dtype("cuda")
+        half = getattr(x, "_soup_half", None)
+        if half is None or half.dtype != dtype or half.shape != x.shape:
+            half = x.to(dtype)
+        for layer in (self.gate_proj, self.up_proj, self.down_proj):
+            if not layer.compute_type_is_set:
+                layer.set_compute_type(x)
+                layer.compute_type_is_set = True
+        return RecomputedMLP.apply(
+            half, self.gate_proj.weight.view(-1), self.gate_proj.weight.quant_state,
+            self.up_proj.weight.view(-1), self.up_proj.weight.quant_state,
+            self.down_proj.weight.view(-1), self.down_proj.weight.quant_state)
+
+    forward._nf4_recompute = True
+    cls.forward = forward

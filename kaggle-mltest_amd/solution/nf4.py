@@ -1,0 +1,184 @@
+"""NF4 dequantization and the 4-bit linear layer on the gfx950 HIP kernels.
+
+Mirror of /root/reference/solution/nf4.py: the same names and signatures (`dequantize_nf4`,
+`NF4Linear`, `patch_linear4bit`, `patch_bnb_matmul_4bit`, `_supported`, `_nf4_state_ok`,
+`_gemm_dtype`, `_base_uses_fused_kernel_for`), the same routing rules, and the same fall-back to
+bitsandbytes' original function for anything this path does not cover.  Underneath, the
+reference's Triton dequant + cuBLAS GEMM becomes one fused dequant-GEMM launch
+(`nf4_linear_fwd` / `nf4_linear_dx` in libnf4_mi355x.so): the fp16 weight is never written
+to HBM.
+
+Differences from the reference, by design:
+* the double-quantized absmax is rebuilt inside the kernels from the uint8 codes (no cached
+  fp32 absmax, nf4.py:41-55), bit for bit the same value;
+* the GEMM runs in fp16 or bf16 only; an fp32 GEMM (the reference's path when neither autocast
+  nor a half compute dtype is set) is left to bitsandbytes' original forward.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+from ._lib import NF4Unsupported
+from .quant_state import nf4_state_ok
+
+DEQUANT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def dequantize_nf4(packed, quant_state, dtype=torch.float16):
+    """The [N, K] weight of a 4-bit NF4 layer in `dtype` (nf4.py:69-77)."""
+    if dtype not in DEQUANT_DTYPES:
+        raise TypeError(f"cannot dequantize to {dtype}")
+    return kernels.dequant([(packed.reshape(-1), quant_state)], dtype).view(
+        tuple(quant_state.shape))
+
+
+class NF4Linear(torch.autograd.Function):
+    """`x @ dequant(W).T + bias`, forward and backward, with the weight dequantized inside the
+    GEMM main loop.  Like the reference (nf4.py:80-102) only the packed weight is kept for the
+    backward pass; the weight gets no gradient."""
+
+    @staticmethod
+    def forward(ctx, x, packed, quant_state, bias):
+        if x.dtype not in kernels.GEMM_DTYPES:
+            raise TypeError(f"NF4Linear computes in fp16 or bf16, got {x.dtype}")
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        packed = packed.reshape(-1)
+        b = None if bias is None else bias.to(x.dtype).contiguous()
+        out = kernels.linear_fwd(x2, [(packed, quant_state)], b)
+        ctx.quant_state = quant_state
+        ctx.has_bias_grad = bias is not None and ctx.needs_input_grad[3]
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        ctx.save_for_backward(packed)
+        return out.view(*shape[:-1], out.shape[-1])
+
+    @staticmethod
+    def backward(ctx, grad):
+        (packed,) = ctx.saved_tensors
+        grad_x = grad_bias = None
+        g2 = grad.reshape(-1, grad.shape[-1])
+        if g2.stride(-1) != 1 or g2.stride(0) % 8 or g2.data_ptr() % 16:
+            g2 = g2.contiguous()
+        if ctx.needs_input_grad[0]:
+            dx = kernels.linear_dx(g2, [(packed, ctx.quant_state)])
+            grad_x = dx.view(*grad.shape[:-1], dx.shape[-1])
+        if ctx.has_bias_grad:
+            grad_bias = kernels.bias_grad(g2).to(ctx.bias_dtype)
+        return grad_x, None, None, grad_bias
+
+
+def _base_uses_fused_kernel_for(m, k, quant_state, dtype, device_index):
+    """True where bitsandbytes' own backend would run its fused small-batch 4-bit GEMM
+    (nf4.py:105-118); there the reference keeps bitsandbytes' numerics."""
+    try:
+        from bitsandbytes.backends.cuda import ops as cuda_ops
+    except Exception:  # noqa: BLE001 - no such backend: nothing to defer to
+        return False
+    n = quant_state.shape[0]
+    try:
+        if m > cuda_ops._gemm_4bit_custom_max_m or k % quant_state.blocksize != 0:
+            return False
+        return bool(cuda_ops._gemm_4bit_use_custom_fn(device_index, dtype, m, n, k))
+    except Exception:  # noqa: BLE001 - a different bitsandbytes: be conservative
+        return True
+
+
+def _base_uses_fused_kernel(x, quant_state, dtype=None):
+    k = x.shape[-1]
+    return _base_uses_fused_kernel_for(x.numel() // k, k, quant_state, dtype or x.dtype,
+                                       x.device.index)
+
+
+def _nf4_state_ok(packed, quant_state, in_features):
+    return nf4_state_ok(packed, quant_state, in_features)
+
+
+def _fused_ok(quant_state) -> bool:
+    """The layouts the fused GEMM covers: each 64-wide step of a weight row inside one absmax
+    block (blocksize a multiple of 64 dividing in_features)."""
+    bs, k = int(quant_state.blocksize), int(quant_state.shape[1])
+    return bs % 64 == 0 and k % bs == 0
+
+
+def _supported(x, packed, quant_state):
+    return (x.is_cuda and x.numel() > 0 and x.dtype in (torch.float16, torch.float32,
+                                                        torch.bfloat16)
+            and _nf4_state_ok(packed, quant_state, x.shape[-1]) and _fused_ok(quant_state))
+
+
+def _gemm_dtype(module, x):
+    """The dtype the base run's GEMM runs in: autocast's when it is on, the layer's compute
+    dtype otherwise (nf4.py:140-145)."""
+    if torch.is_autocast_enabled(x.device.type):
+        return torch.get_autocast_dtype(x.device.type)
+    return module.compute_dtype or x.dtype
+
+
+def patch_linear4bit():
+    """Linear4bit.forward through NF4Linear (nf4.py:148-195).  Needs bitsandbytes; raises
+    ImportError without it (apply() logs that and goes on)."""
+    from bitsandbytes.nn import modules as bnb_modules
+
+    cls = bnb_modules.Linear4bit
+    if getattr(cls.forward, "_nf4_patched", False):
+        return
+    original = cls.forward
+    fix_state = bnb_modules.fix_4bit_weight_quant_state_from_module
+
+    def forward(self, x):
+        if type(self) is not cls and type(self).forward is not forward:
+            return original(self, x)
+        fix_state(self)
+        quant_state = self.weight.quant_state
+        if not x.is_cuda or not _supported(x, self.weight, quant_state):
+            return original(self, x)
+        if not self.compute_type_is_set:
+            self.set_compute_type(x)
+            self.compute_type_is_set = True
+        gemm_dtype = _gemm_dtype(self, x)
+        base_dtype = self.compute_dtype or x.dtype
+        if gemm_dtype not in kernels.GEMM_DTYPES or \
+                _base_uses_fused_kernel(x, quant_state, base_dtype):
+            return original(self, x)
+        half = getattr(x, "_soup_half", None)
+        x = half if half is not None and half.dtype == gemm_dtype and half.shape == x.shape \
+            else x.to(gemm_dtype)
+        bias = self.bias
+        if bias is not None:
+            if bias.dtype != base_dtype:  # as Linear4bit.forward does to its bias
+                bias.data = bias.data.to(base_dtype)
+            bias = bias.to(gemm_dtype)
+        try:
+            return NF4Linear.apply(x, self.weight.view(-1), quant_state, bias)
+        except NF4Unsupported:
+            return original(self, x)
+
+    forward._nf4_patched = True
+    cls.forward = forward
+
+
+def patch_bnb_matmul_4bit():
+    """bitsandbytes.matmul_4bit through NF4Linear (nf4.py:198-216)."""
+    import bitsandbytes
+    from bitsandbytes.autograd import _functions as bnb_autograd
+
+    if getattr(bitsandbytes.matmul_4bit, "_nf4_patched", False):
+        return
+    original = bitsandbytes.matmul_4bit
+
+    def matmul_4bit(A, B, quant_state, out=None, bias=None):
+        if out is not None or not _supported(A, B, quant_state) or \
+                A.dtype not in kernels.GEMM_DTYPES or _base_uses_fused_kernel(A, quant_state):
+            return original(A, B, quant_state, out=out, bias=bias)
+        try:
+            return NF4Linear.apply(A, B.view(-1), quant_state, bias)
+        except NF4Unsupported:
+            return original(A, B, quant_state, out=out, bias=bias)
+
+    matmul_4bit._nf4_patched = True
+    bitsandbytes.matmul_4bit = matmul_4bit
+    bnb_autograd.matmul_4bit = matmul_4bit

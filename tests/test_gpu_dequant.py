@@ -1,0 +1,121 @@
+"""Standalone NF4 dequant kernel vs the CPU oracle: bit-exact (reference test:
+solution/test_kernels.py:51-59, same shapes)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4_oracle as o
+from tests.golden.make_fixtures import OUT as FIXTURES, load_state
+from tests.gpu_util import banner, oracle_w16, random_weight, to_device_state
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def _bits(t):
+    return t.cpu().view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+def _oracle(packed, qs, dt):
+    from tests.gpu_util import to_oracle_state
+
+    p, st = to_oracle_state(packed, qs)
+    w = o.dequantize(p, st, dt)
+    if dt == "bf16":
+        return torch.from_numpy(w.view(np.int16))
+    if dt == "f16":
+        return torch.from_numpy(w).view(torch.int16)
+    return torch.from_numpy(w).view(torch.int32)
+
+
+def test_fixtures_bit_exact(cuda):
+    from solution.nf4 import dequantize_nf4
+
+    z = np.load(FIXTURES)
+    for name in sorted({k.split("/")[0] for k in z.files}):
+        banner("dequant fixture", name)
+        packed, st = load_state(z, name)
+        p, qs = to_device_state(packed, st, cuda)
+        out = dequantize_nf4(p, qs, torch.float16)
+        assert torch.equal(_bits(out), torch.from_numpy(z[f"{name}/w_f16"]).view(torch.int16))
+        out = dequantize_nf4(p, qs, torch.bfloat16)
+        assert torch.equal(_bits(out), torch.from_numpy(z[f"{name}/w_bf16"].view(np.int16)))
+
+
+@pytest.mark.parametrize("shape", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960)])
+def test_reference_shapes_bit_exact(cuda, shape):
+    from solution.nf4 import dequantize_nf4
+
+    banner("dequant shape", shape)
+    packed, qs = random_weight(*shape, seed=sum(shape), dev=cuda, std=0.05)
+    out = dequantize_nf4(packed, qs, torch.float16)
+    torch.cuda.synchronize()
+    assert out.shape == shape
+    assert torch.equal(_bits(out), _oracle(packed, qs, "f16"))
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("shape,bs", [((7, 9), 64), ((33, 64), 32), ((100, 384), 128),
+                                      ((3, 1000), 256), ((5, 6), 2), ((64, 192), 64)])
+def test_layouts_bit_exact(cuda, dt, nested, shape, bs):
+    from solution.nf4 import dequantize_nf4
+
+    banner("dequant layout", dt, nested, shape, bs)
+    packed, qs = random_weight(*shape, seed=7, dev=cuda, blocksize=bs, nested=nested)
+    out = dequantize_nf4(packed, qs, DT[dt])
+    assert torch.equal(_bits(out), _oracle(packed, qs, dt))
+
+
+def test_stacked_segments_bit_exact(cuda):
+    from solution.layer import _dequant
+
+    banner("dequant stacked q|k|v and gate|up")
+    qkv = [random_weight(n, 1536, seed=100 + i, dev=cuda) for i, n in enumerate((1536, 256, 256))]
+    out = _dequant(qkv, torch.float16)
+    ref = torch.cat([_oracle(p, q, "f16").view(int(q.shape[0]), -1) for p, q in qkv])
+    assert torch.equal(_bits(out), ref)
+    odd = [random_weight(n, 68, seed=200 + i, dev=cuda) for i, n in enumerate((3, 5, 1))]
+    out = _dequant(odd, torch.bfloat16)  # unaligned segment starts: general path
+    ref = torch.cat([_oracle(p, q, "bf16").view(int(q.shape[0]), -1) for p, q in odd])
+    assert torch.equal(_bits(out), ref)
+
+
+def test_unaligned_output_and_empty(cuda):
+    from solution import kernels
+
+    banner("dequant unaligned output / empty")
+    p, qs = random_weight(16, 64, seed=9, dev=cuda)
+    buf = torch.zeros(16 * 64 + 1, dtype=torch.float16, device=cuda)
+    kernels.dequant([(p, qs)], torch.float16, out=buf[1:].view(16, 64))
+    assert torch.equal(_bits(buf[1:]), _oracle(p, qs, "f16"))
+    assert buf[0].item() == 0
+    p0, q0 = random_weight(0, 64, seed=9, dev=cuda)
+    assert kernels.dequant([(p0, q0)], torch.float16).shape == (0, 64)
+
+
+def test_round_to_nearest_even_ties(cuda):
+    """Products that fall exactly halfway between two fp16 / bf16 values (absmax 1, table-driven
+    codes): the conversion must round to even, like the oracle's."""
+    from solution.quant_state import QuantState
+    from solution.nf4 import dequantize_nf4
+
+    banner("dequant RNE ties")
+    ties = [1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -11),
+            2 ** -25, 3 * 2 ** -25, 65520.0, -(1 + 3 * 2 ** -8), 0.1, -0.3, 1.0, 0.0, 2.0,
+            1 + 2 ** -9, 3.0]
+    code = torch.tensor(ties, dtype=torch.float32)
+    n = 128
+    q = (torch.arange(n) % 16).to(torch.uint8)
+    packed = ((q[0::2] << 4) | q[1::2]).contiguous()
+    qs = QuantState(absmax=torch.ones(2, dtype=torch.float32).to(cuda), shape=torch.Size((2, 64)),
+                    code=code.to(cuda), blocksize=64, quant_type="nf4", dtype=torch.float16)
+    p = packed.to(cuda)
+    for dt in ("f16", "bf16"):
+        out = dequantize_nf4(p, qs, DT[dt])
+        st = o.OracleQuantState(absmax=np.ones(2, np.float32), shape=(2, 64), code=code.numpy())
+        ref = o.dequantize(packed.numpy(), st, dt)
+        ref = torch.from_numpy(ref.view(np.int16) if dt == "bf16" else ref.view(np.int16))
+        assert torch.equal(_bits(out), ref), dt

@@ -1,0 +1,149 @@
+"""Fused NF4 dequant-GEMMs (forward and input gradient, with bias and LoRA) vs the fp32 oracle
+on the bit-exact dequantized weight.  Tolerance from the path's contract (fp16 and bf16):
+max |out - ref| / max |ref| <= 1e-2 and mean |out - ref| / mean |ref| <= 1e-3."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4_oracle as o
+from tests.golden.make_fixtures import OUT as FIXTURES, load_state
+from tests.gpu_util import assert_rel, banner, oracle_w16, random_weight, to_device_state
+
+pytestmark = pytest.mark.gpu
+
+QWEN_15B = {"q": (1536, 1536), "k": (256, 1536), "v": (256, 1536), "o": (1536, 1536),
+            "gate": (8960, 1536), "up": (8960, 1536), "down": (1536, 8960)}
+
+
+def _x(m, k, seed, dev, dtype=torch.float16, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(m, k, generator=g) * std).to(dtype).to(dev)
+
+
+def test_fixture_forward_and_dx(cuda):
+    from solution import kernels
+
+    z = np.load(FIXTURES)
+    for name in sorted({k.split("/")[0] for k in z.files}):
+        banner("gemm fixture", name)
+        packed, st = load_state(z, name)
+        p, qs = to_device_state(packed, st, cuda)
+        x = torch.from_numpy(z[f"{name}/x"]).to(cuda)
+        bias = torch.from_numpy(z[f"{name}/bias"]).to(cuda)
+        y = kernels.linear_fwd(x, [(p, qs)], bias)
+        assert_rel(y, torch.from_numpy(z[f"{name}/y_ref"]), what=f"{name} fwd")
+        dy = torch.from_numpy(z[f"{name}/dy"]).to(cuda)
+        dx = kernels.linear_dx(dy, [(p, qs)])
+        assert_rel(dx, torch.from_numpy(z[f"{name}/dx_ref"]), what=f"{name} dx")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("proj", list(QWEN_15B))
+def test_qwen_projection_m2048(cuda, proj, dtype):
+    from solution import kernels
+
+    n, k = QWEN_15B[proj]
+    banner("gemm qwen", proj, n, k, dtype)
+    p, qs = random_weight(n, k, seed=100 + list(QWEN_15B).index(proj), dev=cuda)
+    w = oracle_w16(p, qs, "bf16" if dtype == torch.bfloat16 else "f16")
+    x = _x(2048, k, 1, cuda, dtype)
+    y = kernels.linear_fwd(x, [(p, qs)])
+    assert_rel(y, o.linear_fwd(x, w), what=f"{proj} fwd")
+    dy = _x(2048, n, 2, cuda, dtype, std=1e-3)
+    dx = kernels.linear_dx(dy, [(p, qs)])
+    assert_rel(dx, o.linear_dx(dy, w), what=f"{proj} dx")
+
+
+@pytest.mark.parametrize("m", [1, 37, 129, 300, 2049])
+@pytest.mark.parametrize("n,k", [(100, 256), (1000, 320), (256, 64)])
+def test_ragged_shapes(cuda, m, n, k):
+    from solution import kernels
+
+    banner("gemm ragged", m, n, k)
+    p, qs = random_weight(n, k, seed=m + n + k, dev=cuda)
+    w = oracle_w16(p, qs)
+    x = _x(m, k, 3, cuda)
+    bias = _x(1, n, 4, cuda, std=0.1).view(-1)
+    y = kernels.linear_fwd(x, [(p, qs)], bias)
+    assert_rel(y, o.linear_fwd(x, w, bias), what="fwd")
+    if n % 8 == 0:
+        dy = _x(m, n, 5, cuda, std=1e-3)
+        assert_rel(kernels.linear_dx(dy, [(p, qs)]), o.linear_dx(dy, w), what="dx")
+
+
+def test_stacked_qkv_with_bias_and_lora(cuda):
+    from solution import kernels
+
+    banner("gemm stacked qkv + lora")
+    m, k, r, s = 2048, 1536, 16, 2.0
+    segs = [random_weight(n, k, seed=100 + i, dev=cuda) for i, n in enumerate((1536, 256, 256))]
+    w = torch.cat([oracle_w16(p, q) for p, q in segs])
+    x = _x(m, k, 1, cuda)
+    bias = _x(1, 2048, 6, cuda, std=0.5).view(-1)
+    g = torch.Generator().manual_seed(3)
+    bound = 1 / np.sqrt(k)
+    a_q = ((torch.rand(r, k, generator=g) * 2 - 1) * bound).half().to(cuda)
+    a_v = ((torch.rand(r, k, generator=g) * 2 - 1) * bound).half().to(cuda)
+    g = torch.Generator().manual_seed(4)
+    b_q = (torch.randn(1536, r, generator=g) * 0.01).half().to(cuda)
+    b_v = (torch.randn(256, r, generator=g) * 0.01).half().to(cuda)
+    t_q, t_v = kernels.lora_xa(x, a_q), kernels.lora_xa(x, a_v)
+    assert_rel(t_q, x.float().cpu() @ a_q.float().cpu().t(), what="lora_xa")
+    loras = [kernels.make_lora(0, r, s, t=t_q, b=b_q), kernels.make_lora(2, r, s, t=t_v, b=b_v)]
+    y = kernels.linear_fwd(x, segs, bias, loras)
+    ref = o.linear_fwd(x, w, bias, [(0, 1536, x, a_q, b_q, s), (1792, 256, x, a_v, b_v, s)])
+    assert_rel(y, ref, what="qkv fwd")
+    # the LoRA term alone is visible: compare the difference to the base
+    base = o.linear_fwd(x, w, bias)
+    lora_only = (y.float().cpu() - base)[:, :1536]
+    assert_rel(lora_only, (ref - base)[:, :1536], max_rel=5e-2, mean_rel=5e-2, what="lora part")
+
+    dy = _x(m, 2048, 2, cuda, std=1e-3)
+    da_q = kernels.lora_da(dy[:, :1536], b_q, s)
+    da_v = kernels.lora_da(dy[:, 1792:], b_v, s)
+    assert_rel(da_q, s * dy[:, :1536].float().cpu() @ b_q.float().cpu(), what="lora_da")
+    dl = [kernels.make_lora(0, r, s, a=a_q, da=da_q), kernels.make_lora(2, r, s, a=a_v, da=da_v)]
+    dx = kernels.linear_dx(dy, segs, dl)
+    ref_dx = o.linear_dx(dy, w, [(0, 1536, x, a_q, b_q, s), (1792, 256, x, a_v, b_v, s)])
+    assert_rel(dx, ref_dx, what="qkv dx")
+    ga, gb = o.lora_grads(dy[:, :1536], x, a_q, b_q, s)
+    assert_rel(kernels.lora_wgrad(dy[:, :1536], t_q, s, False), gb, what="dB")
+    assert_rel(kernels.lora_wgrad(x, da_q, 1.0, True), ga, what="dA")
+
+
+def test_dx_accumulate_and_gate_up_stack(cuda):
+    from solution import kernels
+
+    banner("gemm dx accumulate, gate|up stack")
+    m, k = 512, 1536
+    segs = [random_weight(8960, k, seed=104 + i, dev=cuda) for i in range(2)]
+    w = torch.cat([oracle_w16(p, q) for p, q in segs])
+    dy = _x(m, 2 * 8960, 7, cuda, std=1e-3)
+    base = _x(m, k, 8, cuda, std=1e-2)
+    out = base.clone()
+    kernels.linear_dx(dy, segs, out=out, accumulate=True)
+    assert_rel(out, base.float().cpu() + o.linear_dx(dy, w), what="dx accumulate")
+    x = _x(m, k, 9, cuda)
+    assert_rel(kernels.linear_fwd(x, segs), o.linear_fwd(x, w), what="gate|up fwd")
+
+
+def test_bias_grad_and_swiglu(cuda):
+    from solution import kernels
+
+    banner("bias grad, swiglu")
+    dy = _x(300, 200, 10, cuda, std=1e-2)
+    torch.testing.assert_close(kernels.bias_grad(dy).cpu(), dy.float().cpu().sum(0),
+                               rtol=1e-5, atol=1e-5)
+    gu = _x(64, 2 * 96, 11, cuda)
+    h = kernels.swiglu_fwd(gu[:, :96], gu[:, 96:])
+    g, u = gu[:, :96].float().cpu(), gu[:, 96:].float().cpu()
+    torch.testing.assert_close(h.float().cpu(), o.silu(g) * u, rtol=2e-3, atol=2e-3)
+    grad = _x(64, 96, 12, cuda)
+    d = gu.clone()
+    kernels.swiglu_bwd(grad, d[:, :96], d[:, 96:], d[:, :96], d[:, 96:])
+    gg = g.clone().requires_grad_()
+    uu = u.clone().requires_grad_()
+    (o.silu(gg) * uu).backward(grad.float().cpu())
+    torch.testing.assert_close(d[:, :96].float().cpu(), gg.grad, rtol=5e-3, atol=5e-3)
+    torch.testing.assert_close(d[:, 96:].float().cpu(), uu.grad, rtol=5e-3, atol=5e-3)

@@ -1,0 +1,98 @@
+"""The reference's operators on the HIP path: NF4Linear (solution/test_kernels.py:62-75),
+the q|k|v projection with LoRA on q and v (layer.py:871-878, 1072-1090) and RecomputedMLP
+(test_kernels.py:200-221), against fp32 autograd of the oracle formulas."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4_oracle as o
+from tests.gpu_util import assert_rel, banner, oracle_w16, random_weight
+
+pytestmark = pytest.mark.gpu
+
+
+def test_nf4_linear_forward_backward(cuda):
+    """The reference's own test case: x [3, 100, 1536], W [256, 1536] with bias."""
+    from solution.nf4 import NF4Linear
+
+    banner("NF4Linear 3x100x1536 -> 256")
+    p, qs = random_weight(256, 1536, seed=0, dev=cuda, std=0.05)
+    w = oracle_w16(p, qs).float()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 100, 1536, generator=g).half().to(cuda).requires_grad_()
+    bias = torch.randn(256, generator=g).half().to(cuda).requires_grad_()
+    grad = torch.randn(3, 100, 256, generator=g).half().to(cuda)
+    out = NF4Linear.apply(x, p, qs, bias)
+    out.backward(grad)
+    xr = x.detach().float().cpu().requires_grad_()
+    br = bias.detach().float().cpu().requires_grad_()
+    ref = torch.nn.functional.linear(xr, w, br)
+    ref.backward(grad.float().cpu())
+    assert out.shape == (3, 100, 256) and out.dtype == torch.float16
+    assert_rel(out, ref.detach(), what="out")
+    assert_rel(x.grad, xr.grad, what="dx")
+    assert_rel(bias.grad, br.grad, max_rel=1e-3, mean_rel=1e-3, what="dbias")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_qkv_projection_with_lora_grads(cuda, dtype):
+    from solution.layer import LoraAdapter, ProjectionSpec, project
+
+    banner("NF4Projection qkv + LoRA", dtype)
+    m, k, r, alpha = 2048, 1536, 16, 32
+    s = alpha / r
+    segs = [random_weight(n, k, seed=100 + i, dev=cuda) for i, n in enumerate((1536, 256, 256))]
+    wname = "bf16" if dtype == torch.bfloat16 else "f16"
+    w = torch.cat([oracle_w16(pp, q, wname) for pp, q in segs]).float()
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(4, 512, k, generator=g).to(dtype).to(cuda).requires_grad_()
+    bias = (torch.randn(2048, generator=g) * 0.5).to(dtype).to(cuda)
+    g3 = torch.Generator().manual_seed(3)
+    bound = 1 / np.sqrt(k)
+    a_q = ((torch.rand(r, k, generator=g3) * 2 - 1) * bound).to(cuda).requires_grad_()
+    a_v = ((torch.rand(r, k, generator=g3) * 2 - 1) * bound).to(cuda).requires_grad_()
+    g4 = torch.Generator().manual_seed(4)
+    b_q = (torch.randn(1536, r, generator=g4) * 0.01).to(cuda).requires_grad_()
+    b_v = (torch.randn(256, r, generator=g4) * 0.01).to(cuda).requires_grad_()
+    spec = ProjectionSpec(weights=segs, loras=[LoraAdapter(0, s), LoraAdapter(2, s)])
+    y = project(x, spec, bias, (a_q, b_q, a_v, b_v))
+    g2 = torch.Generator().manual_seed(2)
+    dy = (torch.randn(4, 512, 2048, generator=g2) * 1e-3).to(dtype).to(cuda)
+    y.backward(dy)
+
+    # fp32 autograd of the same formula on the CPU
+    xr = x.detach().float().cpu().requires_grad_()
+    leaves = [t.detach().float().cpu().requires_grad_() for t in (a_q, b_q, a_v, b_v)]
+    aq, bq, av, bv = leaves
+    yr = xr @ w.t() + bias.float().cpu()
+    yr = torch.cat([yr[..., :1536] + s * (xr @ aq.t()) @ bq.t(), yr[..., 1536:1792],
+                    yr[..., 1792:] + s * (xr @ av.t()) @ bv.t()], -1)
+    yr.backward(dy.float().cpu())
+    assert_rel(y, yr.detach(), what="y")
+    assert_rel(x.grad, xr.grad, what="dx")
+    for name, got, ref in zip(("dA_q", "dB_q", "dA_v", "dB_v"), (a_q.grad, b_q.grad, a_v.grad,
+                                                                 b_v.grad), leaves):
+        assert got.dtype == torch.float32
+        assert_rel(got, ref.grad, what=name)
+
+
+def test_recomputed_mlp_matches_fp32(cuda):
+    """The reference's MLP test shapes (gate/up 1024x512, down 512x1024, x [1, 200, 512])."""
+    from solution.mlp import RecomputedMLP
+
+    banner("RecomputedMLP")
+    gate = random_weight(1024, 512, seed=1, dev=cuda, std=0.05)
+    up = random_weight(1024, 512, seed=2, dev=cuda, std=0.05)
+    down = random_weight(512, 1024, seed=3, dev=cuda, std=0.05)
+    wg, wu, wd = (oracle_w16(p, q).float() for p, q in (gate, up, down))
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 200, 512, generator=g).half().to(cuda).requires_grad_()
+    grad = torch.randn(1, 200, 512, generator=g).half().to(cuda)
+    out = RecomputedMLP.apply(x, gate[0], gate[1], up[0], up[1], down[0], down[1])
+    out.backward(grad)
+    xr = x.detach().float().cpu().requires_grad_()
+    ref = o.mlp_fwd(xr, wg, wu, wd)
+    ref.backward(grad.float().cpu())
+    assert_rel(out, ref.detach(), what="mlp out")
+    assert_rel(x.grad, xr.grad, what="mlp dx")

@@ -1,0 +1,187 @@
+"""Pins the CPU oracle against what mathematics and library routines fix (no GPU)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4_oracle as o
+
+
+# ------------------------------------------------------------------------------- NF4 table
+
+def test_nf4_table_matches_closed_form():
+    built = o.create_normal_map()
+    assert built.shape == (16,)
+    np.testing.assert_allclose(built, o.NF4_CODE, rtol=0, atol=1e-6)
+
+
+def test_nf4_table_invariants():
+    c = o.NF4_CODE
+    assert c.dtype == np.float32 and c.shape == (16,)
+    assert np.all(np.diff(c) > 0)
+    assert c[0] == -1.0 and c[15] == 1.0 and c[7] == 0.0
+    assert (c > 0).sum() == 8 and (c < 0).sum() == 7
+    # literals are exact fp32 values
+    assert np.all(c.astype(np.float64).astype(np.float32) == c)
+
+
+# ----------------------------------------------------------------------------- dynamic map
+
+def test_dynamic_map_closed_form():
+    d = o.DYNAMIC_CODE.astype(np.float64)
+    assert d.shape == (256,) and np.all(np.diff(d) > 0)
+    assert d[0] < 0 and d[-1] == 1.0 and (d == 0).sum() == 1
+    pos = d[(d > 0) & (d < 1.0)]
+    neg = -d[d < 0][::-1]
+    np.testing.assert_array_equal(np.sort(pos), np.sort(neg))
+    expected = []
+    for i in range(7):
+        b = np.linspace(0.1, 1.0, 2 ** i + 1)
+        expected += list(10.0 ** (i - 6) * (b[:-1] + b[1:]) / 2)
+    np.testing.assert_allclose(np.sort(pos), np.sort(expected), rtol=1e-6)
+    # per decade: 2**i values in (10**(i-6) * 0.1, 10**(i-6)]
+    for i in range(7):
+        lo, hi = 10.0 ** (i - 6) * 0.1, 10.0 ** (i - 6)
+        assert ((pos > lo) & (pos <= hi)).sum() == 2 ** i
+
+
+# -------------------------------------------------------------------------------- dequant
+
+def _small(shape=(24, 128), seed=0, scale=0.02, bs=64, nested=True):
+    w = np.random.default_rng(seed).standard_normal(shape).astype(np.float32) * scale
+    return w, *o.quantize_nf4(w, blocksize=bs, compress_statistics=nested)
+
+
+@pytest.mark.parametrize("nested", [True, False])
+@pytest.mark.parametrize("shape,bs", [((24, 128), 64), ((5, 7), 64), ((3, 33), 2), ((17, 256), 128)])
+def test_dequant_vectorised_equals_element_loop(shape, bs, nested):
+    _, packed, st = _small(shape, bs=bs, nested=nested)
+    np.testing.assert_array_equal(o.dequantize(packed, st, "f16"), o.dequantize_loop(packed, st))
+
+
+def test_absmax_rebuild_matches_scalar_loop():
+    _, packed, st = _small((40, 512))
+    a = o.absmax_fp32(st)
+    for b in range(st.absmax.size):
+        prod = np.float32(st.state2.code[st.absmax[b]]) * np.float32(st.state2.absmax[b // 256])
+        assert a[b] == np.float32(np.float32(prod) + np.float32(st.offset))
+
+
+def test_absmax_rebuild_has_no_fma():
+    # a case where fma(x, y, z) and fp32(fp32(x*y) + z) differ: the oracle must give the latter
+    x, y, z = np.float32(1.0 + 2 ** -12), np.float32(1.0 + 2 ** -12), np.float32(-1.0)
+    prod = np.float32(x * y)
+    separate = np.float32(prod + z)
+    fused = np.float32(np.float64(x) * np.float64(y) + np.float64(z))
+    assert separate != fused
+    st = o.OracleQuantState(absmax=np.array([1], np.uint8), shape=(1, 64), nested=True,
+                            offset=float(z),
+                            state2=o.OracleState2(absmax=np.array([y], np.float32),
+                                                  code=np.array([0.0, x] + [0.0] * 254,
+                                                                np.float32)))
+    assert o.absmax_fp32(st)[0] == separate
+
+
+def test_dequant_conversions_match_torch():
+    _, packed, st = _small((64, 256))
+    f32 = o.dequantize_f32(packed, st)
+    t = torch.from_numpy(f32)
+    np.testing.assert_array_equal(o.dequantize(packed, st, "f16"), t.half().numpy())
+    bf = torch.from_numpy(o.dequantize(packed, st, "bf16").view(np.int16)).view(torch.bfloat16)
+    assert torch.equal(bf, t.bfloat16())
+
+
+def test_bf16_rounding_ties_to_even():
+    vals = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8), 1.0 + 2 ** -9,
+                     3.0e38, 1e-40], np.float32)
+    ours = torch.from_numpy(o.f32_to_bf16_bits(vals).view(np.int16)).view(torch.bfloat16)
+    assert torch.equal(ours, torch.from_numpy(vals).bfloat16())
+
+
+def test_dequant_special_cases():
+    # absmax exactly 1.0 (no double quant): every element is its code value rounded to fp16
+    n = 64
+    q = np.arange(n, dtype=np.uint8) % 16
+    packed = ((q[0::2] << 4) | q[1::2]).astype(np.uint8)
+    st = o.OracleQuantState(absmax=np.ones(1, np.float32), shape=(1, n))
+    out = o.dequantize(packed, st, "f16").reshape(-1)
+    np.testing.assert_array_equal(out, o.NF4_CODE[q].astype(np.float16))
+    # code 7 is zero whatever the absmax; code 15 gives the absmax itself
+    st.absmax = np.array([3.5], np.float32)
+    out = o.dequantize(packed, st, "f16").reshape(-1)
+    assert np.all(out[q == 7] == 0) and np.all(out[q == 15] == np.float16(3.5))
+    assert np.all(out[q == 0] == np.float16(-3.5))
+    # high nibble first: byte 0xF0 -> [code15, code0]
+    st = o.OracleQuantState(absmax=np.ones(1, np.float32), shape=(1, 2))
+    np.testing.assert_array_equal(o.dequantize(np.array([0xF0], np.uint8), st, "f16").reshape(-1),
+                                  np.array([1.0, -1.0], np.float16))
+
+
+def test_quantize_roundtrip_error_bound():
+    w, packed, st = _small((64, 512), seed=3)
+    deq = o.dequantize_f32(packed, st).reshape(-1)
+    a = o.absmax_fp32(st)
+    true_absmax = np.abs(w.reshape(-1, 64)).max(1)
+    # per block: |w - deq| <= |a| * half the widest NF4 gap + |a - true absmax|
+    err = np.abs(w.reshape(-1) - deq).reshape(-1, 64).max(1)
+    bound = np.abs(a) * o.nf4_max_gap() + np.abs(a - true_absmax) + 1e-7
+    assert np.all(err <= bound)
+    # the double-quantized absmax is close to the true one (8-bit dynamic code)
+    assert np.max(np.abs(a - true_absmax) / true_absmax) < 0.02
+
+
+def test_quantize_zero_block():
+    w = np.zeros((2, 64), np.float32)
+    w[1] = np.linspace(-1, 1, 64, dtype=np.float32)
+    packed, st = o.quantize_nf4(w)
+    deq = o.dequantize_f32(packed, st)
+    assert np.all(o.nibbles(packed, 128)[:64] == 7)
+    assert np.all(np.isfinite(deq))
+
+
+def test_quantize_nearest_code():
+    x = np.array([-1.0, -0.9, 0.0, 0.03, 0.05, 0.99, 1.0], np.float32)
+    got = o.quantize_nf4_codes(x)
+    brute = np.array([np.argmin(np.abs(o.NF4_CODE.astype(np.float64) - v)) for v in x])
+    np.testing.assert_array_equal(got, brute)
+
+
+# ------------------------------------------------------------------------ GEMM / LoRA refs
+
+def test_lora_backward_formulas_match_autograd():
+    g = torch.Generator().manual_seed(0)
+    m, k, n, r, s = 9, 32, 24, 4, 2.0
+    x = torch.randn(m, k, generator=g, requires_grad=True)
+    w = torch.randn(n, k, generator=g)
+    a = torch.randn(r, k, generator=g, requires_grad=True)
+    b = torch.randn(8, r, generator=g, requires_grad=True)
+    lor = [(4, 8, x, a, b, s)]
+    y = x @ w.t()
+    y = torch.cat([y[:, :4], y[:, 4:12] + s * (x @ a.t()) @ b.t(), y[:, 12:]], 1)
+    dy = torch.randn(m, n, generator=g)
+    y.backward(dy)
+    ref_fwd = o.linear_fwd(x.detach(), w, None, [(4, 8, x.detach(), a.detach(), b.detach(), s)])
+    torch.testing.assert_close(ref_fwd, y.detach())
+    dx = o.linear_dx(dy, w, [(4, 8, None, a.detach(), b.detach(), s)])
+    torch.testing.assert_close(dx, x.grad)
+    ga, gb = o.lora_grads(dy[:, 4:12], x.detach(), a.detach(), b.detach(), s)
+    torch.testing.assert_close(ga, a.grad)
+    torch.testing.assert_close(gb, b.grad)
+    assert lor
+
+
+def test_mlp_reference_matches_autograd_composition():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(5, 16, generator=g)
+    wg, wu, wd = (torch.randn(32, 16, generator=g), torch.randn(32, 16, generator=g),
+                  torch.randn(16, 32, generator=g))
+    ref = torch.nn.functional.linear(
+        torch.nn.functional.silu(x @ wg.t()) * (x @ wu.t()), wd)
+    torch.testing.assert_close(o.mlp_fwd(x, wg, wu, wd), ref)
+
+
+def test_rel_errors_definition():
+    ref = torch.tensor([1.0, -2.0, 4.0])
+    out = torch.tensor([1.0, -2.0, 4.4])
+    mx, mean = o.rel_errors(out, ref)
+    assert abs(mx - 0.1) < 1e-6 and abs(mean - (0.4 / 3) / (7 / 3)) < 1e-6
