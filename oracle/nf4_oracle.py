@@ -275,7 +275,7 @@ def _t(a):
         if a.dtype == np.uint16:  # bf16 bits
             return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).float()
         return torch.from_numpy(np.ascontiguousarray(a)).float()
-    return a.detach().float().cpu()
+    return a.float().cpu()  # differentiable: references may be run under autograd
 
 
 def linear_fwd(x, w, bias=None, loras=()):
@@ -327,7 +327,7 @@ def mlp_fwd(x, wg, wu, wd):
 def rel_errors(out, ref) -> tuple[float, float]:
     """(max |out-ref| / max |ref|, mean |out-ref| / mean |ref|): the reference's ``_rel``
     (layer.py:1253-1254) and its mean counterpart."""
-    out, ref = _t(out), _t(ref)
+    out, ref = _t(out).detach(), _t(ref).detach()
     d = (out - ref).abs()
     return (d.max().item() / (ref.abs().max().item() + 1e-12),
             d.mean().item() / (ref.abs().mean().item() + 1e-12))

@@ -59,6 +59,11 @@ def oracle_w16(packed, qs, dtype="f16"):
 
 
 def assert_rel(out, ref, max_rel=1e-2, mean_rel=1e-3, what=""):
+    """The path's tolerance.  fp16 (the contract): max rel <= 1e-2, mean rel <= 1e-3.  A bf16
+    output's own rounding (8 significant bits) already gives mean rel ~1.4e-3, so bf16 results
+    are held to mean rel <= 3e-3 (max rel unchanged)."""
+    if getattr(out, "dtype", None) == torch.bfloat16:
+        mean_rel = max(mean_rel, 3e-3)
     mx, mean = o.rel_errors(out, ref)
     assert mx <= max_rel and mean <= mean_rel, f"{what}: max rel {mx:.3e}, mean rel {mean:.3e}"
     return mx, mean
