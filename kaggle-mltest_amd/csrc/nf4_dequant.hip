@@ -152,8 +152,12 @@ int launch(DequantArgs &a, bool fast, int dt, hipStream_t stream) {
 
 extern "C" int nf4_dequant_multi(const nf4_weight *ws, int nw, void *out, int out_dtype,
                                  void *stream) {
-    if (!ws || nw < 1 || nw > NF4_MAX_SEGMENTS || !out) return NF4_ERR_ARG;
+    if (!ws || nw < 1 || nw > NF4_MAX_SEGMENTS) return NF4_ERR_ARG;
     if (out_dtype != NF4_F16 && out_dtype != NF4_BF16 && out_dtype != NF4_F32) return NF4_ERR_ARG;
+    int64_t total = 0;
+    for (int i = 0; i < nw; ++i) total += ws[i].rows * ws[i].cols;
+    if (total == 0) return NF4_OK;  // nothing to write (out may be null)
+    if (!out) return NF4_ERR_ARG;
     const int dts = dtype_bytes(out_dtype);
     DequantArgs a = {};
     a.nseg = nw;

@@ -13,21 +13,34 @@
 // With v_mfma_f32_32x32x16 each lane then owns one activation row m and four consecutive p,
 // so results leave as 8-byte row-major stores of Y[m, n..n+3] or dX[m, k..k+3].
 //
-// Tiles: BP x BM outputs per workgroup, reduction step BR = 64 (one NF4 absmax block along k
-// for the forward weight).  Both operand tiles are double-buffered in LDS with rows padded to
-// 144 bytes (conflict-free 16-byte fragment reads).  Per step the next tile's global loads are
-// issued before the MFMAs of the current one; the weight bytes are dequantized (NF4 table in
-// LDS, absmax rebuilt from its uint8 code, fp32 product, one RNE conversion) when they are
-// written to LDS.  Long reductions are split over workgroups into fp32 partial sums that a
-// reduction kernel adds up in a fixed order (deterministic).
+// Workgroup tile BP x BM, reduction step 64 (one NF4 absmax block along k for the forward
+// weight), two LDS stages.  LDS tiles are rows of 64 16-bit values (128 bytes) whose 16-byte
+// chunks are XOR-swizzled by the row index, so MFMA fragment reads of 32 consecutive rows spread
+// over the banks.  Per step:
+//   * the activation tile of the next step streams straight from global memory into the other
+//     LDS stage (global_load_lds_dwordx4, no registers; lanes pick their global chunk so that
+//     the lane-linear LDS writes land in the swizzled layout);
+//   * the packed weight bytes of the next step (4x smaller than fp16) are prefetched into
+//     registers;
+//   * the MFMAs of the current step run; meanwhile the other wave on the same SIMD dequantizes
+//     (NF4 table in LDS, absmax rebuilt from its uint8 code, fp32 product, one RNE conversion)
+//     and writes the next weight tile to LDS;
+//   * one barrier.
+// Long reductions are split over workgroups into fp32 partial sums that a reduction kernel
+// adds up in a fixed order (deterministic).
 
 #include "nf4_common.h"
 
 namespace {
 
-constexpr int BR = 64;          // reduction step
-constexpr int SROW = 72;        // LDS row stride in 16-bit elements (64 + 8 pad)
+constexpr int BR = 64;           // reduction step
+constexpr int ROWB = 128;        // bytes per LDS tile row
 constexpr int kMaxSeg = NF4_MAX_SEGMENTS;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Byte offset of 16-byte chunk c (elements 8c..8c+7) of row r in an LDS tile.
+__device__ __forceinline__ int swz(int r, int c) { return r * ROWB + ((c ^ (r & 7)) << 4); }
 
 struct LoraDev {
     const uint16_t *t;   // forward: [M, rank]
@@ -114,63 +127,94 @@ __device__ __forceinline__ int seg_of_step(const GemmArgs &a, int64_t t) {
     return s;
 }
 
-// Activation tile [BM rows][64] from act[m][col0 .. col0+64) (columns >= col_end read as 0).
-template <int BM, int NT>
-struct ActLoader {
-    static constexpr int CH = BM * 8 / NT;  // 16-byte chunks per thread
-    u32x4_t r[CH];
-
-    __device__ __forceinline__ void load(const GemmArgs &a, int64_t m0, int64_t col0,
-                                         int64_t col_end) {
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int idx = i * NT + threadIdx.x;
-            const int64_t m = m0 + (idx >> 3);
-            const int64_t c = col0 + (idx & 7) * 8;
-            u32x4_t v = {0u, 0u, 0u, 0u};
-            if (m < a.M) {
-                const uint16_t *src = a.act + m * a.ld_act + c;
-                if (c + 8 <= col_end) {
-                    v = *reinterpret_cast<const u32x4_t *>(src);
-                } else if (c < col_end) {
-                    uint16_t e[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) e[j] = (c + j < col_end) ? src[j] : 0;
-                    v.x = e[0] | (uint32_t(e[1]) << 16);
-                    v.y = e[2] | (uint32_t(e[3]) << 16);
-                    v.z = e[4] | (uint32_t(e[5]) << 16);
-                    v.w = e[6] | (uint32_t(e[7]) << 16);
-                }
-            }
-            r[i] = v;
-        }
-    }
-
-    __device__ __forceinline__ void store(uint16_t *s) const {
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int idx = i * NT + threadIdx.x;
-            *reinterpret_cast<u32x4_t *>(s + (idx >> 3) * SROW + (idx & 7) * 8) = r[i];
-        }
-    }
+// The raw absmax inputs of block b, fetched with the packed bytes; rebuilt later by absmax_val.
+struct AbsIn {
+    float s;      // absmax2 scale (nested) or the fp32 absmax
+    uint32_t q;   // uint8 code (nested)
 };
+
+__device__ __forceinline__ AbsIn absmax_load(const DevWeight &w, int64_t b) {
+    AbsIn r;
+    if (w.nested) {
+        r.q = static_cast<const uint8_t *>(w.absmax)[b];
+        r.s = w.absmax2[b / w.blocksize2];
+    } else {
+        r.q = 0;
+        r.s = static_cast<const float *>(w.absmax)[b];
+    }
+    return r;
+}
+
+__device__ __forceinline__ float absmax_val(const DevWeight &w, const AbsIn &in, const float *code2) {
+    return w.nested ? __fadd_rn(__fmul_rn(code2[in.q], in.s), w.offset) : in.s;
+}
+
+// ------------------------------------------------------------------ activation tile loader
+
+// BM rows x 64 columns of act[m][col0 ..] into an LDS tile.  Full-width steps stream straight
+// into LDS; rows past M re-read row M-1 (their results are never stored).
+template <int BM, int NT>
+__device__ __forceinline__ void act_load_direct(const GemmArgs &a, uint8_t *s, int64_t m0,
+                                                int64_t col0) {
+    constexpr int REGIONS = BM * ROWB / 1024;   // 1 KB = 8 rows per wave instruction
+    constexpr int WAVES = NT / 64;
+    static_assert(REGIONS % WAVES == 0, "tile rows must split evenly over the waves");
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < REGIONS / WAVES; ++i) {
+        const int region = i * WAVES + wave;
+        const int r = region * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ (r & 7);      // this lane's slot holds logical chunk c
+        int64_t m = m0 + r;
+        m = m < a.M ? m : a.M - 1;
+        __builtin_amdgcn_global_load_lds(a.act + m * a.ld_act + col0 + c * 8,
+                                         (lds_void *)(s + region * 1024), 16, 0, 0);
+    }
+}
+
+// Same tile with columns >= col_end read as zero (a segment's last, partial reduction step).
+template <int BM, int NT>
+__device__ __forceinline__ void act_load_masked(const GemmArgs &a, uint8_t *s, int64_t m0,
+                                                int64_t col0, int64_t col_end) {
+    for (int idx = threadIdx.x; idx < BM * 8; idx += NT) {
+        const int r = idx >> 3, c = idx & 7;
+        const int64_t m = m0 + r;
+        const int64_t cc = col0 + c * 8;
+        uint16_t e[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (m < a.M) {
+            const uint16_t *src = a.act + m * a.ld_act + cc;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (cc + j < col_end) e[j] = src[j];
+        }
+        u32x4_t v;
+        v.x = e[0] | (uint32_t(e[1]) << 16);
+        v.y = e[2] | (uint32_t(e[3]) << 16);
+        v.z = e[4] | (uint32_t(e[5]) << 16);
+        v.w = e[6] | (uint32_t(e[7]) << 16);
+        *reinterpret_cast<u32x4_t *>(s + swz(r, c)) = v;
+    }
+}
+
+// ------------------------------------------------------------------------- MFMA core
 
 // Wave-level MFMA over one 64-deep step: acc[TP][TM] += Wop[p rows] x Act[m rows].
 template <int DT, int TP, int TM>
-__device__ __forceinline__ void mma_step(float16_t (&acc)[TP][TM], const uint16_t *sw,
-                                         const uint16_t *sa, int prow0, int mrow0) {
+__device__ __forceinline__ void mma_step(float16_t (&acc)[TP][TM], const uint8_t *sw,
+                                         const uint8_t *sa, int prow0, int mrow0) {
     const int lane = threadIdx.x & 63;
     const int r = lane & 31;
-    const int kh = (lane >> 5) * 8;
+    const int kh = lane >> 5;
 #pragma unroll
     for (int ks = 0; ks < BR / 16; ++ks) {
+        const int c = ks * 2 + kh;
         u32x4_t fa[TP], fb[TM];
 #pragma unroll
         for (int i = 0; i < TP; ++i)
-            fa[i] = *reinterpret_cast<const u32x4_t *>(sw + (prow0 + i * 32 + r) * SROW + ks * 16 + kh);
+            fa[i] = *reinterpret_cast<const u32x4_t *>(sw + swz(prow0 + i * 32 + r, c));
 #pragma unroll
         for (int j = 0; j < TM; ++j)
-            fb[j] = *reinterpret_cast<const u32x4_t *>(sa + (mrow0 + j * 32 + r) * SROW + ks * 16 + kh);
+            fb[j] = *reinterpret_cast<const u32x4_t *>(sa + swz(mrow0 + j * 32 + r, c));
 #pragma unroll
         for (int i = 0; i < TP; ++i)
 #pragma unroll
@@ -253,16 +297,90 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
     }
 }
 
-// ------------------------------------------------------------------------------- forward
+// ------------------------------------------------------------------------ weight tiles
+
+// Forward weight tile: BP rows x 64 k of W (natural layout).  Thread t owns 16 packed bytes =
+// 32 elements of row t/2 (one absmax); NT == 2 * BP.
+template <int DT, int BP>
+struct FwdWeight {
+    u32x4_t raw;
+    AbsIn abs;
+
+    __device__ __forceinline__ void load(const DevWeight &w, int64_t p0, int64_t K, int64_t st) {
+        const int row = threadIdx.x >> 1;
+        const int64_t n = p0 + row;
+        raw = (u32x4_t){0u, 0u, 0u, 0u};
+        abs = AbsIn{0.f, 0u};
+        if (n < w.rows) {
+            const int64_t e0 = n * K + st * BR;
+            raw = *reinterpret_cast<const u32x4_t *>(w.packed + (e0 >> 1) + (threadIdx.x & 1) * 16);
+            abs = absmax_load(w, e0 / w.blocksize);
+        }
+    }
+
+    __device__ __forceinline__ void store(const DevWeight &w, uint8_t *s, const float *code,
+                                          const float *code2) const {
+        const int row = threadIdx.x >> 1, h = (threadIdx.x & 1) * 4;
+        const float sc = absmax_val(w, abs, code2);
+        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 0)) = dequant8<DT>(raw.x, sc, code);
+        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 1)) = dequant8<DT>(raw.y, sc, code);
+        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 2)) = dequant8<DT>(raw.z, sc, code);
+        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 3)) = dequant8<DT>(raw.w, sc, code);
+    }
+};
+
+// dX weight tile: 64 n x BP k of W, written transposed (LDS rows = k).  Thread t owns a patch
+// of 4 rows n x 8 columns k (one dword per row, one absmax per row); NT == 2 * BP.
+template <int DT, int BP>
+struct DxWeight {
+    static constexpr int KG = BP / 8;
+    uint32_t raw[4];
+    AbsIn abs[4];
+
+    __device__ __forceinline__ void load(const DevWeight &w, int64_t n0, int64_t p0, int64_t K) {
+        const int kg = threadIdx.x % KG, ng = threadIdx.x / KG;
+        const int64_t k = p0 + kg * 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t n = n0 + ng * 4 + i;
+            raw[i] = 0u;
+            abs[i] = AbsIn{0.f, 0u};
+            if (n < w.rows && k < K) {
+                const int64_t e0 = n * K + k;
+                raw[i] = *reinterpret_cast<const uint32_t *>(w.packed + (e0 >> 1));
+                abs[i] = absmax_load(w, e0 / w.blocksize);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(const DevWeight &w, uint8_t *s, const float *code,
+                                          const float *code2) const {
+        const int kg = threadIdx.x % KG, ng = threadIdx.x / KG;
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[i] = absmax_val(w, abs[i], code2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int sh = (e & 1) ? (e >> 1) * 8 : (e >> 1) * 8 + 4;
+            u32x2_t o;
+            o.x = pack2<DT>(__fmul_rn(code[(raw[0] >> sh) & 0xF], sc[0]),
+                            __fmul_rn(code[(raw[1] >> sh) & 0xF], sc[1]));
+            o.y = pack2<DT>(__fmul_rn(code[(raw[2] >> sh) & 0xF], sc[2]),
+                            __fmul_rn(code[(raw[3] >> sh) & 0xF], sc[3]));
+            *reinterpret_cast<u32x2_t *>(s + swz(kg * 8 + e, ng >> 1) + (ng & 1) * 8) = o;
+        }
+    }
+};
+
+// ------------------------------------------------------------------------------- kernels
 
 template <int DT, int BP, int BM, int WP, int WM>
 __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     constexpr int NT = WP * WM * 64;
     constexpr int TP = BP / WP / 32, TM = BM / WM / 32;
-    constexpr int WCH = BP * 2 / NT;  // 16-byte packed chunks (32 elements) per thread
-    static_assert(WCH >= 1 && BP * 2 % NT == 0, "weight tile too small for the workgroup");
-    __shared__ __attribute__((aligned(16))) uint16_t sW[2][BP * SROW];
-    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * SROW];
+    static_assert(NT == 2 * BP, "forward weight tile mapping needs 2 threads per row");
+    __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BP * ROWB];
+    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
     __shared__ float s_code[16];
     __shared__ float s_code2[256];
 
@@ -274,7 +392,6 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const int64_t p0 = (local / a.m_tiles) * BP;
     const int64_t m0 = (local % a.m_tiles) * BM;
     const DevWeight &w = a.w[seg];
-    const int64_t rows = w.rows;
     const int64_t K = a.K;
     const int64_t steps = K / BR;
     const int64_t per = (steps + a.splits - 1) / a.splits;
@@ -305,8 +422,8 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < TP; ++i) {
                 const int64_t p = p0 + wp * (BP / WP) + i * 32 + r;
-                fa[i] = (p < rows && lim > 0) ? gather8(lo.b + p * lo.rank + k0 + kh, 1, lim)
-                                              : (u32x4_t){0u, 0u, 0u, 0u};
+                fa[i] = (p < w.rows && lim > 0) ? gather8(lo.b + p * lo.rank + k0 + kh, 1, lim)
+                                                : (u32x4_t){0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
@@ -325,73 +442,38 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
             for (int j = 0; j < TM; ++j) acc[i][j] *= lo.scale;
     }
 
-    ActLoader<BM, NT> al;
-    u32x4_t wr[WCH];
-    auto wload = [&](int64_t st) {
-#pragma unroll
-        for (int i = 0; i < WCH; ++i) {
-            const int idx = i * NT + threadIdx.x;
-            const int64_t n = p0 + (idx >> 1);
-            wr[i] = (u32x4_t){0u, 0u, 0u, 0u};
-            if (n < rows)
-                wr[i] = *reinterpret_cast<const u32x4_t *>(
-                    w.packed + ((n * K + st * BR) >> 1) + (idx & 1) * 16);
-        }
-    };
-    auto wstore = [&](uint16_t *s, int64_t st) {
-#pragma unroll
-        for (int i = 0; i < WCH; ++i) {
-            const int idx = i * NT + threadIdx.x;
-            const int64_t n = p0 + (idx >> 1);
-            const float sc = n < rows ? absmax_of(w, s_code2, (n * K + st * BR) / w.blocksize) : 0.f;
-            uint16_t *d = s + (idx >> 1) * SROW + (idx & 1) * 32;
-            *reinterpret_cast<u32x4_t *>(d + 0) = dequant8<DT>(wr[i].x, sc, s_code);
-            *reinterpret_cast<u32x4_t *>(d + 8) = dequant8<DT>(wr[i].y, sc, s_code);
-            *reinterpret_cast<u32x4_t *>(d + 16) = dequant8<DT>(wr[i].z, sc, s_code);
-            *reinterpret_cast<u32x4_t *>(d + 24) = dequant8<DT>(wr[i].w, sc, s_code);
-        }
-    };
-
+    FwdWeight<DT, BP> wt;
     __syncthreads();  // tables
     if (s0 < s1) {
-        al.load(a, m0, s0 * BR, K);
-        wload(s0);
-        al.store(sA[0]);
-        wstore(sW[0], s0);
+        act_load_direct<BM, NT>(a, sA[0], m0, s0 * BR);
+        wt.load(w, p0, K, s0);
+        wt.store(w, sW[0], s_code, s_code2);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         for (int64_t st = s0; st < s1; ++st) {
             const int buf = static_cast<int>((st - s0) & 1);
             const bool more = st + 1 < s1;
             if (more) {
-                al.load(a, m0, (st + 1) * BR, K);
-                wload(st + 1);
+                act_load_direct<BM, NT>(a, sA[buf ^ 1], m0, (st + 1) * BR);
+                wt.load(w, p0, K, st + 1);
             }
             mma_step<DT, TP, TM>(acc, sW[buf], sA[buf], wp * (BP / WP), wm * (BM / WM));
-            if (more) {
-                al.store(sA[buf ^ 1]);
-                wstore(sW[buf ^ 1], st + 1);
-            }
+            if (more) wt.store(w, sW[buf ^ 1], s_code, s_code2);
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
     }
-    epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), rows, a.seg_off[seg],
+    epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), w.rows, a.seg_off[seg],
                          m0 + wm * (BM / WM), split);
 }
-
-// ---------------------------------------------------------------------------- dX (W^T)
 
 template <int DT, int BP, int BM, int WP, int WM>
 __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     constexpr int NT = WP * WM * 64;
     constexpr int TP = BP / WP / 32, TM = BM / WM / 32;
-    // The weight tile of one step is [64 n][BP k]; each thread dequantizes one patch of
-    // 8 n x PK k (PK = 8: one dword per row, PK = 4: one 16-bit word per row) and writes it
-    // transposed as PK LDS rows of 8 consecutive n.
-    constexpr int PK = BP * 64 / (NT * 8);
-    static_assert((PK == 4 || PK == 8) && BP * 64 == NT * 8 * PK, "unsupported dX tile");
-    constexpr int KG = BP / PK;            // k-groups per step
-    __shared__ __attribute__((aligned(16))) uint16_t sW[2][BP * SROW];
-    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * SROW];
+    static_assert(NT == 2 * BP, "dX weight tile mapping needs 2 threads per k column group");
+    __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BP * ROWB];
+    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
     __shared__ float s_code[kMaxSeg][16];
     __shared__ float s_code2[kMaxSeg][256];
 
@@ -450,75 +532,32 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
         }
     }
 
-    ActLoader<BM, NT> al;
-    uint32_t wr[8];
-    float wsc[8];
-    int wseg = 0;
-    const int kl = (threadIdx.x % KG) * PK;
-    const int nl = (threadIdx.x / KG) * 8;
-    auto wload = [&](int64_t st, int seg) {
-        const DevWeight &w = a.w[seg];
-        const int64_t n0 = (st - a.step_start[seg]) * BR + nl;
-        const int64_t k = p0 + kl;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t n = n0 + i;
-            wr[i] = 0u;
-            wsc[i] = 0.f;
-            if (n < w.rows && k < K) {
-                const uint8_t *src = w.packed + ((n * K + k) >> 1);
-                if constexpr (PK == 8) wr[i] = *reinterpret_cast<const uint32_t *>(src);
-                else wr[i] = *reinterpret_cast<const uint16_t *>(src);
-                wsc[i] = absmax_of(w, s_code2[seg], (n * K + k) / w.blocksize);
-            }
-        }
-    };
-    auto wstore = [&](uint16_t *s, int seg) {
-        const float *code = s_code[seg];
-        // element e of row i: byte e/2 of wr[i], high nibble for even e
-#pragma unroll
-        for (int e = 0; e < PK; ++e) {
-            const int sh = (e & 1) ? (e >> 1) * 8 : (e >> 1) * 8 + 4;
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = __fmul_rn(code[(wr[i] >> sh) & 0xF], wsc[i]);
-            u32x4_t o;
-            o.x = pack2<DT>(v[0], v[1]);
-            o.y = pack2<DT>(v[2], v[3]);
-            o.z = pack2<DT>(v[4], v[5]);
-            o.w = pack2<DT>(v[6], v[7]);
-            *reinterpret_cast<u32x4_t *>(s + (kl + e) * SROW + nl) = o;
-        }
+    DxWeight<DT, BP> wt;
+    // One reduction step: segment seg, rows n0 .. n0+64 of it.
+    auto load_step = [&](int64_t st, uint8_t *sa_buf, int &seg) {
+        seg = seg_of_step(a, st);
+        const int64_t n0 = (st - a.step_start[seg]) * BR;
+        const int64_t rows = a.w[seg].rows;
+        const int64_t col0 = a.seg_off[seg] + n0;
+        if (n0 + BR <= rows) act_load_direct<BM, NT>(a, sa_buf, m0, col0);
+        else act_load_masked<BM, NT>(a, sa_buf, m0, col0, a.seg_off[seg] + rows);
+        wt.load(a.w[seg], n0, p0, K);
     };
 
     __syncthreads();  // tables
     if (s0 < s1) {
-        wseg = seg_of_step(a, s0);
-        {
-            const int64_t n0 = (s0 - a.step_start[wseg]) * BR;
-            al.load(a, m0, a.seg_off[wseg] + n0, a.seg_off[wseg] + a.w[wseg].rows);
-        }
-        wload(s0, wseg);
-        al.store(sA[0]);
-        wstore(sW[0], wseg);
+        int seg;
+        load_step(s0, sA[0], seg);
+        wt.store(a.w[seg], sW[0], s_code[seg], s_code2[seg]);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         for (int64_t st = s0; st < s1; ++st) {
             const int buf = static_cast<int>((st - s0) & 1);
             const bool more = st + 1 < s1;
-            int nseg_next = wseg;
-            if (more) {
-                nseg_next = seg_of_step(a, st + 1);
-                const int64_t n0 = (st + 1 - a.step_start[nseg_next]) * BR;
-                al.load(a, m0, a.seg_off[nseg_next] + n0,
-                        a.seg_off[nseg_next] + a.w[nseg_next].rows);
-                wload(st + 1, nseg_next);
-            }
+            if (more) load_step(st + 1, sA[buf ^ 1], seg);
             mma_step<DT, TP, TM>(acc, sW[buf], sA[buf], wp * (BP / WP), wm * (BM / WM));
-            if (more) {
-                al.store(sA[buf ^ 1]);
-                wstore(sW[buf ^ 1], nseg_next);
-                wseg = nseg_next;
-            }
+            if (more) wt.store(a.w[seg], sW[buf ^ 1], s_code[seg], s_code2[seg]);
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
     }
@@ -547,7 +586,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial,
 // ------------------------------------------------------------------------------ host side
 
 struct Plan {
-    int cfg;       // 0: 256x256 tile, 1: 128x128 tile
+    int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves
     int bp, bm;
     int splits;
     int64_t tiles;
@@ -577,15 +616,27 @@ int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const n
     return NF4_OK;
 }
 
-int choose_splits(int64_t tiles, int64_t steps) {
+// Splits of the reduction so that about one round of workgroups covers the GPU, keeping at
+// least 8 steps per split.
+int choose_splits(int64_t tiles, int64_t steps, int per_cu) {
     int s = 1;
-    while (tiles * s < kCUs && steps / (s * 2) >= 8 && s < 16) s *= 2;
+    while (tiles * s * 2 <= kCUs * per_cu && steps / (s * 2) >= 8 && s < 16) s *= 2;
     return s;
 }
 
-Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
+Plan make_plan(int64_t big, int64_t small, int64_t steps) {
     Plan p{};
-    const int64_t steps = ws[0].cols / BR;
+    if (big >= kCUs) {
+        p.cfg = 0; p.bp = 256; p.bm = 256; p.tiles = big;
+        p.splits = choose_splits(big, steps, 1);
+    } else {
+        p.cfg = 1; p.bp = 128; p.bm = 128; p.tiles = small;
+        p.splits = choose_splits(small, steps, 2);
+    }
+    return p;
+}
+
+Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
     int64_t big = 0, small = 0;
     for (int i = 0; i < nw; ++i) {
         big += (ws[i].rows + 255) / 256;
@@ -593,36 +644,23 @@ Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
     }
     big *= (m + 255) / 256;
     small *= (m + 127) / 128;
-    if (big >= 2 * kCUs) {
-        p.cfg = 0; p.bp = 256; p.bm = 256; p.tiles = big;
-    } else {
-        p.cfg = 1; p.bp = 128; p.bm = 128; p.tiles = small;
-    }
-    p.splits = choose_splits(p.tiles, steps);
-    return p;
+    return make_plan(big, small, ws[0].cols / BR);
 }
 
 Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
-    Plan p{};
     int64_t steps = 0;
     for (int i = 0; i < nw; ++i) steps += (ws[i].rows + BR - 1) / BR;
     const int64_t K = ws[0].cols;
     const int64_t big = ((K + 255) / 256) * ((m + 255) / 256);
     const int64_t small = ((K + 127) / 128) * ((m + 127) / 128);
-    if (big >= 2 * kCUs) {
-        p.cfg = 0; p.bp = 256; p.bm = 256; p.tiles = big;
-    } else {
-        p.cfg = 1; p.bp = 128; p.bm = 128; p.tiles = small;
-    }
-    p.splits = choose_splits(p.tiles, steps);
-    return p;
+    return make_plan(big, small, steps);
 }
 
 template <int DT>
 int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.tiles * p.splits));
     if (p.cfg == 0)
-        hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 2>), grid, dim3(256), 0, st, g);
+        hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
     else
         hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2>), grid, dim3(256), 0, st, g);
     return status_of(hipGetLastError());
@@ -632,7 +670,7 @@ template <int DT>
 int launch_dx(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.tiles * p.splits));
     if (p.cfg == 0)
-        hipLaunchKernelGGL((dx_kernel<DT, 256, 256, 2, 2>), grid, dim3(256), 0, st, g);
+        hipLaunchKernelGGL((dx_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
     else
         hipLaunchKernelGGL((dx_kernel<DT, 128, 128, 2, 2>), grid, dim3(256), 0, st, g);
     return status_of(hipGetLastError());

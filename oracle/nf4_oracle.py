@@ -239,7 +239,8 @@ def dequantize(packed: np.ndarray, state: OracleQuantState, dtype: str = "f16") 
     ``"f32"`` -> float32 (nf4.py:69-77 with ``dtype``)."""
     v = dequantize_f32(packed, state)
     if dtype == "f16":
-        return v.astype(np.float16)
+        with np.errstate(over="ignore"):  # beyond fp16 range rounds to +-inf, as on the GPU
+            return v.astype(np.float16)
     if dtype == "bf16":
         return f32_to_bf16_bits(v)
     if dtype == "f32":

@@ -64,9 +64,12 @@ def test_version_and_status_strings(lib):
 def test_argument_validation_without_launch(lib):
     from solution._lib import NF4_ERR_ARG, NF4Weight
 
-    w = NF4Weight()
+    empty = NF4Weight(blocksize=64)
+    assert lib.nf4_dequant(ctypes.byref(empty), None, 0, None) == 0  # nothing to do
+    w = NF4Weight(rows=4, cols=64, blocksize=64)  # non-empty with null pointers
     assert lib.nf4_dequant(None, None, 0, None) == NF4_ERR_ARG
     assert lib.nf4_dequant(ctypes.byref(w), None, 0, None) == NF4_ERR_ARG
+    assert lib.nf4_dequant(ctypes.byref(w), ctypes.c_void_p(16), 0, None) == NF4_ERR_ARG
     assert lib.nf4_dequant_multi(ctypes.byref(w), 0, ctypes.c_void_p(16), 0, None) == NF4_ERR_ARG
     assert lib.nf4_linear_fwd(None, 4, 64, ctypes.byref(w), 1, None, None, 0, None, 64, 0, None,
                               0, None) == NF4_ERR_ARG

@@ -74,7 +74,9 @@ def test_qkv_projection_with_lora_grads(cuda, dtype):
     for name, got, ref in zip(("dA_q", "dB_q", "dA_v", "dB_v"), (a_q.grad, b_q.grad, a_v.grad,
                                                                  b_v.grad), leaves):
         assert got.dtype == torch.float32
-        assert_rel(got, ref.grad, what=name)
+        # fp32 gradients from half-precision operands (da is rounded to the GEMM dtype, as the
+        # reference's fp16 da is): bf16 operands carry the bf16 mean tolerance
+        assert_rel(got, ref.grad, mean_rel=3e-3 if dtype == torch.bfloat16 else 1e-3, what=name)
 
 
 def test_recomputed_mlp_matches_fp32(cuda):
