@@ -32,7 +32,16 @@ struct DevWeight {
     int64_t cols;
     int32_t blocksize;
     int32_t blocksize2;
+    int32_t bs_shift;   // log2(blocksize) if a power of two, else -1
+    int32_t bs2_shift;  // log2(blocksize2) if a power of two, else -1
 };
+
+static inline int log2_exact(int64_t v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int s = 0;
+    while ((int64_t(1) << s) < v) ++s;
+    return s;
+}
 
 static inline DevWeight to_dev(const nf4_weight &w) {
     DevWeight d;
@@ -47,7 +56,18 @@ static inline DevWeight to_dev(const nf4_weight &w) {
     d.cols = w.cols;
     d.blocksize = w.blocksize;
     d.blocksize2 = w.blocksize2;
+    d.bs_shift = log2_exact(w.blocksize);
+    d.bs2_shift = log2_exact(w.blocksize2);
     return d;
+}
+
+// Absmax block of element e and absmax2 group of block b: shifts for power-of-two sizes (every
+// blocksize bitsandbytes produces), a division otherwise.
+__device__ __forceinline__ int64_t block_index(const DevWeight &w, int64_t e) {
+    return w.bs_shift >= 0 ? (e >> w.bs_shift) : e / w.blocksize;
+}
+__device__ __forceinline__ int64_t group_index(const DevWeight &w, int64_t b) {
+    return w.bs2_shift >= 0 ? (b >> w.bs2_shift) : b / w.blocksize2;
 }
 
 // The fp32 absmax of block b: fp32(code2[q] * absmax2[b / blocksize2]) + offset, each operation
@@ -55,7 +75,7 @@ static inline DevWeight to_dev(const nf4_weight &w) {
 __device__ __forceinline__ float absmax_of(const DevWeight &w, const float *code2_lds, int64_t b) {
     if (w.nested) {
         const uint8_t q = static_cast<const uint8_t *>(w.absmax)[b];
-        const float s = w.absmax2[b / w.blocksize2];
+        const float s = w.absmax2[group_index(w, b)];
         return __fadd_rn(__fmul_rn(code2_lds[q], s), w.offset);
     }
     return static_cast<const float *>(w.absmax)[b];
@@ -75,6 +95,69 @@ template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     if constexpr (DT == NF4_BF16) return pack2_bf16(a, b);
     else return pack2_f16(a, b);
+}
+
+// ---------------------------------------------------------- register-table NF4 lookup
+//
+// For one absmax s, the 16 possible dequantized values round(code[i] * s) (each the same single
+// fp32 product and single RNE rounding as the element-wise formula) are packed into byte planes:
+// lo[k] holds the low bytes of entries 4k..4k+3, hi[k] their high bytes.  v_perm_b32 then picks
+// 4 entries at once by nibble: two perms select within entries 0-7 and 8-15, a third chooses
+// between them by bit 3 of each nibble, and two more interleave low and high bytes into
+// 16-bit pairs.  No LDS access and no latency chain.
+
+static constexpr uint32_t kPermLoBytes = 0x06040200u;  // bytes 0,2 of S1 and of S0
+static constexpr uint32_t kPermHiBytes = 0x07050301u;  // bytes 1,3 of S1 and of S0
+
+struct Nf4Table {
+    uint32_t lo[4];
+    uint32_t hi[4];
+};
+
+__device__ __forceinline__ uint32_t vperm(uint32_t s0, uint32_t s1, uint32_t sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+template <int DT>
+__device__ __forceinline__ Nf4Table make_table(const float (&code)[16], float s) {
+    uint32_t t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = pack2<DT>(__fmul_rn(code[2 * j], s), __fmul_rn(code[2 * j + 1], s));
+    Nf4Table r;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        r.lo[k] = vperm(t[2 * k + 1], t[2 * k], kPermLoBytes);
+        r.hi[k] = vperm(t[2 * k + 1], t[2 * k], kPermHiBytes);
+    }
+    return r;
+}
+
+// 4 nibbles s (one per byte, element order) -> 4 table entries as two packed pairs.
+__device__ __forceinline__ void lookup4(const Nf4Table &t, uint32_t s, uint32_t &o0, uint32_t &o1) {
+    const uint32_t s7 = s & 0x07070707u;
+    const uint32_t sel = ((s >> 1) & 0x04040404u) | 0x03020100u;  // byte i: i, or 4 + i if bit 3
+    const uint32_t lo = vperm(vperm(t.lo[3], t.lo[2], s7), vperm(t.lo[1], t.lo[0], s7), sel);
+    const uint32_t hi = vperm(vperm(t.hi[3], t.hi[2], s7), vperm(t.hi[1], t.hi[0], s7), sel);
+    o0 = vperm(hi, lo, 0x05010400u);
+    o1 = vperm(hi, lo, 0x07030602u);
+}
+
+// The 8 elements of one packed dword (byte j: high nibble = element 2j, low = 2j+1), as four
+// packed 16-bit pairs in element order.
+__device__ __forceinline__ u32x4_t lookup8(const Nf4Table &t, uint32_t p) {
+    const uint32_t hi4 = (p >> 4) & 0x0F0F0F0Fu;   // byte j: element 2j
+    const uint32_t lo4 = p & 0x0F0F0F0Fu;          // byte j: element 2j + 1
+    uint32_t o0, o1, o2, o3;
+    lookup4(t, vperm(lo4, hi4, 0x05010400u), o0, o1);  // elements 0..3
+    lookup4(t, vperm(lo4, hi4, 0x07030602u), o2, o3);  // elements 4..7
+    return (u32x4_t){o0, o1, o2, o3};
+}
+
+// The NF4 table of a weight in scalar registers (the same for every lane).
+__device__ __forceinline__ void load_code_sgpr(const float *code, float (&out)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        out[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, code[i])));
 }
 
 static inline int status_of(hipError_t e) { return e == hipSuccess ? NF4_OK : NF4_ERR_LAUNCH; }

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void dequant_units_kernel(const DequantAr
 #pragma unroll
     for (int g = 0; g < kUnroll; ++g) {
         if (u[g] < units) {
-            const float s = absmax_of(w, s_code2, (u[g] << 3) / w.blocksize);
+            const float s = absmax_of(w, s_code2, block_index(w, u[g] << 3));
             float v[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kThreads) void dequant_units_kernel(const DequantAr
             for (int64_t e = units << 3; e < n; ++e) {
                 const uint8_t byte = w.packed[e >> 1];
                 const int nib = (e & 1) ? (byte & 0xF) : (byte >> 4);
-                const float s = absmax_of(w, s_code2, e / w.blocksize);
+                const float s = absmax_of(w, s_code2, block_index(w, e));
                 store1<DT>(out, off + e, __fmul_rn(s_code[nib], s));
             }
         }
@@ -123,28 +123,28 @@ __global__ __launch_bounds__(kThreads) void dequant_elements_kernel(const Dequan
     for (int64_t e = lb * kThreads + threadIdx.x; e < n; e += nblocks * kThreads) {
         const uint8_t byte = w.packed[e >> 1];
         const int nib = (e & 1) ? (byte & 0xF) : (byte >> 4);
-        const float s = absmax_of(w, s_code2, e / w.blocksize);
+        const float s = absmax_of(w, s_code2, block_index(w, e));
         store1<DT>(a.out, a.out_off[seg] + e, __fmul_rn(s_code[nib], s));
     }
 }
 
-template <template <int> class K>
-struct Launcher;
+enum Path { kElements = 0, kUnits = 1 };
 
-int launch(DequantArgs &a, bool fast, int dt, hipStream_t stream) {
+template <int DT>
+void launch_dt(const DequantArgs &a, int path, dim3 g, hipStream_t stream) {
+    const dim3 b(kThreads);
+    if (path == kUnits) hipLaunchKernelGGL(dequant_units_kernel<DT>, g, b, 0, stream, a);
+    else hipLaunchKernelGGL(dequant_elements_kernel<DT>, g, b, 0, stream, a);
+}
+
+int launch(DequantArgs &a, int path, int dt, hipStream_t stream) {
     const int64_t grid = a.block_start[a.nseg];
     if (grid == 0) return NF4_OK;
     if (grid > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
-    dim3 g(static_cast<unsigned>(grid)), b(kThreads);
-    if (fast) {
-        if (dt == NF4_F16) hipLaunchKernelGGL(dequant_units_kernel<NF4_F16>, g, b, 0, stream, a);
-        else if (dt == NF4_BF16) hipLaunchKernelGGL(dequant_units_kernel<NF4_BF16>, g, b, 0, stream, a);
-        else hipLaunchKernelGGL(dequant_units_kernel<NF4_F32>, g, b, 0, stream, a);
-    } else {
-        if (dt == NF4_F16) hipLaunchKernelGGL(dequant_elements_kernel<NF4_F16>, g, b, 0, stream, a);
-        else if (dt == NF4_BF16) hipLaunchKernelGGL(dequant_elements_kernel<NF4_BF16>, g, b, 0, stream, a);
-        else hipLaunchKernelGGL(dequant_elements_kernel<NF4_F32>, g, b, 0, stream, a);
-    }
+    const dim3 g(static_cast<unsigned>(grid));
+    if (dt == NF4_F16) launch_dt<NF4_F16>(a, path, g, stream);
+    else if (dt == NF4_BF16) launch_dt<NF4_BF16>(a, path, g, stream);
+    else launch_dt<NF4_F32>(a, path, g, stream);
     return status_of(hipGetLastError());
 }
 
@@ -163,7 +163,7 @@ extern "C" int nf4_dequant_multi(const nf4_weight *ws, int nw, void *out, int ou
     a.nseg = nw;
     a.out = out;
     int64_t off = 0;
-    bool fast = aligned(out, 16);
+    bool units_ok = aligned(out, 16);
     for (int i = 0; i < nw; ++i) {
         const int st = check_weight(&ws[i]);
         if (st != NF4_OK) return st;
@@ -171,17 +171,18 @@ extern "C" int nf4_dequant_multi(const nf4_weight *ws, int nw, void *out, int ou
         a.w[i] = to_dev(ws[i]);
         a.out_off[i] = off;
         const int64_t n = ws[i].rows * ws[i].cols;
-        fast = fast && (ws[i].blocksize % 8 == 0) && aligned(ws[i].packed, 4) &&
-               ((off * dts) % 16 == 0);
+        const bool out_ok = (off * dts) % 16 == 0;
+        units_ok = units_ok && (ws[i].blocksize % 8 == 0) && aligned(ws[i].packed, 4) && out_ok;
         off += n;
     }
-    // Grid: fast path covers ceil(units (+1 partial) / (threads * unroll)) blocks per segment;
-    // the general path a bounded grid-stride grid.
+    const int path = units_ok ? kUnits : kElements;
+    // Grid: the vector paths cover ceil(units (+1 partial) / (threads * unroll)) workgroups per
+    // segment; the general path a bounded grid-stride grid.
     a.block_start[0] = 0;
     for (int i = 0; i < nw; ++i) {
         const int64_t n = ws[i].rows * ws[i].cols;
         int64_t blocks;
-        if (fast) {
+        if (path == kUnits) {
             const int64_t units = (n >> 3) + ((n & 7) ? 1 : 0);
             blocks = (units + kThreads * kUnroll - 1) / (kThreads * kUnroll);
         } else {
@@ -190,7 +191,7 @@ extern "C" int nf4_dequant_multi(const nf4_weight *ws, int nw, void *out, int ou
         }
         a.block_start[i + 1] = a.block_start[i] + blocks;
     }
-    return launch(a, fast, out_dtype, static_cast<hipStream_t>(stream));
+    return launch(a, path, out_dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int nf4_dequant(const nf4_weight *w, void *out, int out_dtype, void *stream) {

@@ -37,10 +37,11 @@ constexpr int BR = 64;           // reduction step
 constexpr int ROWB = 128;        // bytes per LDS tile row
 constexpr int kMaxSeg = NF4_MAX_SEGMENTS;
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Byte offset of 16-byte chunk c (elements 8c..8c+7) of row r in an LDS tile.
-__device__ __forceinline__ int swz(int r, int c) { return r * ROWB + ((c ^ (r & 7)) << 4); }
+// Byte offset of 16-byte chunk c (elements 8c..8c+7) of row r in an LDS tile.  gfx950's LDS
+// serves a 16-byte-per-lane access 16 lanes (256 bytes, 64 banks) at a time; XOR-ing the chunk
+// with bits 1..3 of the row makes the 16 rows such a group reads (an MFMA fragment: 16
+// consecutive rows, one chunk) land on 16 distinct (row parity, chunk) bank slots.
+__device__ __forceinline__ int swz(int r, int c) { return r * ROWB + ((c ^ ((r >> 1) & 7)) << 4); }
 
 struct LoraDev {
     const uint16_t *t;   // forward: [M, rank]
@@ -55,6 +56,7 @@ struct LoraDev {
 struct GemmArgs {
     const uint16_t *act;          // X (forward) or dY (dx)
     int64_t ld_act;
+    int64_t act_cols;             // valid columns of a row of act (forward: K; dx: sum rows)
     int64_t M;
     int64_t K;                    // in_features of every segment
     DevWeight w[kMaxSeg];
@@ -133,67 +135,136 @@ struct AbsIn {
     uint32_t q;   // uint8 code (nested)
 };
 
-__device__ __forceinline__ AbsIn absmax_load(const DevWeight &w, int64_t b) {
-    AbsIn r;
-    if (w.nested) {
-        r.q = static_cast<const uint8_t *>(w.absmax)[b];
-        r.s = w.absmax2[b / w.blocksize2];
-    } else {
-        r.q = 0;
-        r.s = static_cast<const float *>(w.absmax)[b];
-    }
-    return r;
-}
-
 __device__ __forceinline__ float absmax_val(const DevWeight &w, const AbsIn &in, const float *code2) {
     return w.nested ? __fadd_rn(__fmul_rn(code2[in.q], in.s), w.offset) : in.s;
 }
 
-// ------------------------------------------------------------------ activation tile loader
+// ----------------------------------------------------------------- buffer resources
+//
+// Main-loop loads go through buffer resources: an offset at or past the resource's byte range
+// returns zero in hardware.  Every lane then issues the same unconditional loads (no divergent
+// branches in the pipeline, so the compiler's wait counters stay exact), rows past M and weight
+// rows past the segment read as zero, and nothing outside an operand is ever touched.
 
-// BM rows x 64 columns of act[m][col0 ..] into an LDS tile.  Full-width steps stream straight
-// into LDS; rows past M re-read row M-1 (their results are never stored).
-template <int BM, int NT>
-__device__ __forceinline__ void act_load_direct(const GemmArgs &a, uint8_t *s, int64_t m0,
-                                                int64_t col0) {
-    constexpr int REGIONS = BM * ROWB / 1024;   // 1 KB = 8 rows per wave instruction
-    constexpr int WAVES = NT / 64;
-    static_assert(REGIONS % WAVES == 0, "tile rows must split evenly over the waves");
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-    for (int i = 0; i < REGIONS / WAVES; ++i) {
-        const int region = i * WAVES + wave;
-        const int r = region * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ (r & 7);      // this lane's slot holds logical chunk c
-        int64_t m = m0 + r;
-        m = m < a.M ? m : a.M - 1;
-        __builtin_amdgcn_global_load_lds(a.act + m * a.ld_act + col0 + c * 8,
-                                         (lds_void *)(s + region * 1024), 16, 0, 0);
-    }
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+    const int n = bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : static_cast<int>(bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), n,
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4_t bload16(rsrc_t r, int off) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload2(rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload1(rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
 }
 
-// Same tile with columns >= col_end read as zero (a segment's last, partial reduction step).
-template <int BM, int NT>
-__device__ __forceinline__ void act_load_masked(const GemmArgs &a, uint8_t *s, int64_t m0,
-                                                int64_t col0, int64_t col_end) {
-    for (int idx = threadIdx.x; idx < BM * 8; idx += NT) {
-        const int r = idx >> 3, c = idx & 7;
-        const int64_t m = m0 + r;
-        const int64_t cc = col0 + c * 8;
-        uint16_t e[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (m < a.M) {
-            const uint16_t *src = a.act + m * a.ld_act + cc;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (cc + j < col_end) e[j] = src[j];
-        }
-        u32x4_t v;
-        v.x = e[0] | (uint32_t(e[1]) << 16);
-        v.y = e[2] | (uint32_t(e[3]) << 16);
-        v.z = e[4] | (uint32_t(e[5]) << 16);
-        v.w = e[6] | (uint32_t(e[7]) << 16);
-        *reinterpret_cast<u32x4_t *>(s + swz(r, c)) = v;
+// Resources of one weight: packed bytes, uint8 absmax codes (nested) and the fp32 scale array
+// (absmax2 when nested, the fp32 absmax otherwise).
+struct WeightRsrc {
+    rsrc_t packed, q, s;
+    int nested;
+    int bs_shift, bs2_shift;
+};
+
+__device__ __forceinline__ WeightRsrc weight_rsrc(const DevWeight &w) {
+    const int64_t n = w.rows * w.cols;
+    const int64_t nb = (n + w.blocksize - 1) / w.blocksize;
+    WeightRsrc r;
+    r.packed = make_rsrc(w.packed, (n + 1) / 2);
+    r.nested = w.nested;
+    r.bs_shift = w.bs_shift;
+    r.bs2_shift = w.bs2_shift;
+    if (w.nested) {
+        r.q = make_rsrc(w.absmax, nb);
+        r.s = make_rsrc(w.absmax2, ((nb + w.blocksize2 - 1) / w.blocksize2) * 4);
+    } else {
+        r.q = make_rsrc(w.absmax, 0);
+        r.s = make_rsrc(w.absmax, nb * 4);
     }
+    return r;
+}
+
+// The absmax inputs of block b: uint8 code + absmax2 scale (nested) or the fp32 absmax.
+__device__ __forceinline__ AbsIn absmax_bload(const WeightRsrc &r, int64_t b) {
+    AbsIn a;
+    a.q = bload1(r.q, static_cast<int>(b));
+    const int64_t si = r.nested ? (b >> r.bs2_shift) : b;
+    a.s = __builtin_bit_cast(float, bload4(r.s, static_cast<int>(si * 4)));
+    return a;
+}
+
+// ------------------------------------------------------------------ activation tile loader
+
+// BM rows x 64 columns of act[m][col0 ..] staged through registers: load() issues the global
+// loads of a step (16 bytes per chunk, 8 consecutive threads per 128-byte row), store() writes
+// them to an LDS tile after the current step's MFMAs, so the wait for the loads lands there.
+// Rows >= M and columns >= col_end read as zero.
+template <int BM, int NT>
+struct ActTile {
+    static constexpr int CH = BM * 8 / NT;
+    static_assert(CH >= 1 && BM * 8 % NT == 0, "tile rows must split evenly over the threads");
+    u32x4_t r[CH];
+
+    // `rs` covers rows m0 .. min(M, m0 + BM) of the operand (row stride ld elements); rows past
+    // M come back as zero from the hardware range check.
+    __device__ __forceinline__ void load(rsrc_t rs, int64_t ld, int64_t col0) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int idx = i * NT + threadIdx.x;
+            const int64_t off = (static_cast<int64_t>(idx >> 3) * ld + col0 + (idx & 7) * 8) * 2;
+            r[i] = bload16(rs, static_cast<int>(off));
+        }
+    }
+
+    // Zero the elements at columns >= col_end (a segment's last, partial reduction step).
+    __device__ __forceinline__ void mask(int64_t col0, int64_t col_end) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int idx = i * NT + threadIdx.x;
+            const int64_t k = col_end - (col0 + (idx & 7) * 8);  // valid elements of the chunk
+            uint32_t w[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t lo = (2 * d < k) ? 0x0000ffffu : 0u;
+                const uint32_t hi = (2 * d + 1 < k) ? 0xffff0000u : 0u;
+                w[d] &= lo | hi;
+            }
+            r[i] = (u32x4_t){w[0], w[1], w[2], w[3]};
+        }
+    }
+
+    __device__ __forceinline__ void store(uint8_t *s) const {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int idx = i * NT + threadIdx.x;
+            *reinterpret_cast<u32x4_t *>(s + swz(idx >> 3, idx & 7)) = r[i];
+        }
+    }
+
+    // Chunks i with i % 4 == part (one quarter of the tile per MFMA k-substep).
+    __device__ __forceinline__ void store_part(uint8_t *s, int part) const {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            if (i % 4 != part) continue;
+            const int idx = i * NT + threadIdx.x;
+            *reinterpret_cast<u32x4_t *>(s + swz(idx >> 3, idx & 7)) = r[i];
+        }
+    }
+};
+
+// Resource over the BM-row activation window of a workgroup.
+template <int BM>
+__device__ __forceinline__ rsrc_t act_rsrc(const GemmArgs &a, int64_t m0) {
+    const int64_t rows = a.M - m0 < BM ? a.M - m0 : BM;
+    return make_rsrc(a.act + m0 * a.ld_act, ((rows - 1) * a.ld_act + a.act_cols) * 2);
 }
 
 // ------------------------------------------------------------------------- MFMA core
@@ -219,6 +290,34 @@ __device__ __forceinline__ void mma_step(float16_t (&acc)[TP][TM], const uint8_t
         for (int i = 0; i < TP; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j) acc[i][j] = mfma32<DT>(fa[i], fb[j], acc[i][j]);
+    }
+}
+
+// mma_step with part ks of the next tile's staging work (`part(ks)`: global-to-LDS copy and
+// dequantization of data already in registers) placed among the MFMAs of k-substep ks, so the
+// VALU and LDS-write work runs while the matrix unit is busy.
+template <int DT, int TP, int TM, class Part>
+__device__ __forceinline__ void mma_step_interleaved(float16_t (&acc)[TP][TM], const uint8_t *sw,
+                                                     const uint8_t *sa, int prow0, int mrow0,
+                                                     Part &&part) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31;
+    const int kh = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < BR / 16; ++ks) {
+        const int c = ks * 2 + kh;
+        u32x4_t fa[TP], fb[TM];
+#pragma unroll
+        for (int i = 0; i < TP; ++i)
+            fa[i] = *reinterpret_cast<const u32x4_t *>(sw + swz(prow0 + i * 32 + r, c));
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+            fb[j] = *reinterpret_cast<const u32x4_t *>(sa + swz(mrow0 + j * 32 + r, c));
+#pragma unroll
+        for (int i = 0; i < TP; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc[i][j] = mfma32<DT>(fa[i], fb[j], acc[i][j]);
+        part(ks);
     }
 }
 
@@ -306,16 +405,11 @@ struct FwdWeight {
     u32x4_t raw;
     AbsIn abs;
 
-    __device__ __forceinline__ void load(const DevWeight &w, int64_t p0, int64_t K, int64_t st) {
-        const int row = threadIdx.x >> 1;
-        const int64_t n = p0 + row;
-        raw = (u32x4_t){0u, 0u, 0u, 0u};
-        abs = AbsIn{0.f, 0u};
-        if (n < w.rows) {
-            const int64_t e0 = n * K + st * BR;
-            raw = *reinterpret_cast<const u32x4_t *>(w.packed + (e0 >> 1) + (threadIdx.x & 1) * 16);
-            abs = absmax_load(w, e0 / w.blocksize);
-        }
+    // Rows past the weight read as zero (their outputs are never stored).
+    __device__ __forceinline__ void load(const WeightRsrc &r, int64_t p0, int64_t K, int64_t st) {
+        const int64_t e0 = (p0 + (threadIdx.x >> 1)) * K + st * BR;
+        raw = bload16(r.packed, static_cast<int>((e0 >> 1) + (threadIdx.x & 1) * 16));
+        abs = absmax_bload(r, e0 >> r.bs_shift);
     }
 
     __device__ __forceinline__ void store(const DevWeight &w, uint8_t *s, const float *code,
@@ -327,50 +421,87 @@ struct FwdWeight {
         *reinterpret_cast<u32x4_t *>(s + swz(row, h + 2)) = dequant8<DT>(raw.z, sc, code);
         *reinterpret_cast<u32x4_t *>(s + swz(row, h + 3)) = dequant8<DT>(raw.w, sc, code);
     }
+
+    // Dword `part` of the 16 packed bytes (8 elements) through the register table of this
+    // thread's row (make_table with the row's absmax).
+    __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, int part) const {
+        const int row = threadIdx.x >> 1, h = (threadIdx.x & 1) * 4;
+        const uint32_t wd = part == 0 ? raw.x : part == 1 ? raw.y : part == 2 ? raw.z : raw.w;
+        *reinterpret_cast<u32x4_t *>(s + swz(row, h + part)) = lookup8(tb, wd);
+    }
 };
 
-// dX weight tile: 64 n x BP k of W, written transposed (LDS rows = k).  Thread t owns a patch
-// of 4 rows n x 8 columns k (one dword per row, one absmax per row); NT == 2 * BP.
+// dX weight tile: 64 rows n x BP columns k of W in its natural layout (rows of BP 16-bit values;
+// 16-byte chunk c of row n at chunk c ^ 4 (n & 3)).  Thread t dequantizes 32 consecutive k of
+// row t / (BP / 32): one absmax, one register table, four 16-byte LDS writes, as the forward
+// tile.  The MFMA reads it transposed (mma_step_dx below).
+template <int BP>
+__device__ __forceinline__ int swz_t(int n, int c) {
+    return n * (BP * 2) + ((c ^ ((n & 3) << 2)) << 4);
+}
+
 template <int DT, int BP>
 struct DxWeight {
-    static constexpr int KG = BP / 8;
-    uint32_t raw[4];
-    AbsIn abs[4];
+    static constexpr int KQ = BP / 32;   // threads per tile row
+    u32x4_t raw;
+    AbsIn abs;
 
-    __device__ __forceinline__ void load(const DevWeight &w, int64_t n0, int64_t p0, int64_t K) {
-        const int kg = threadIdx.x % KG, ng = threadIdx.x / KG;
-        const int64_t k = p0 + kg * 8;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t n = n0 + ng * 4 + i;
-            raw[i] = 0u;
-            abs[i] = AbsIn{0.f, 0u};
-            if (n < w.rows && k < K) {
-                const int64_t e0 = n * K + k;
-                raw[i] = *reinterpret_cast<const uint32_t *>(w.packed + (e0 >> 1));
-                abs[i] = absmax_load(w, e0 / w.blocksize);
-            }
-        }
+    // Rows past the segment read as zero; columns past K read neighbouring bytes (their
+    // outputs are never stored).
+    __device__ __forceinline__ void load(const WeightRsrc &r, int64_t n0, int64_t p0, int64_t K) {
+        const int64_t e0 = (n0 + threadIdx.x / KQ) * K + p0 + (threadIdx.x % KQ) * 32;
+        raw = bload16(r.packed, static_cast<int>(e0 >> 1));
+        abs = absmax_bload(r, e0 >> r.bs_shift);
     }
 
-    __device__ __forceinline__ void store(const DevWeight &w, uint8_t *s, const float *code,
-                                          const float *code2) const {
-        const int kg = threadIdx.x % KG, ng = threadIdx.x / KG;
-        float sc[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc[i] = absmax_val(w, abs[i], code2);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int sh = (e & 1) ? (e >> 1) * 8 : (e >> 1) * 8 + 4;
-            u32x2_t o;
-            o.x = pack2<DT>(__fmul_rn(code[(raw[0] >> sh) & 0xF], sc[0]),
-                            __fmul_rn(code[(raw[1] >> sh) & 0xF], sc[1]));
-            o.y = pack2<DT>(__fmul_rn(code[(raw[2] >> sh) & 0xF], sc[2]),
-                            __fmul_rn(code[(raw[3] >> sh) & 0xF], sc[3]));
-            *reinterpret_cast<u32x2_t *>(s + swz(kg * 8 + e, ng >> 1) + (ng & 1) * 8) = o;
-        }
+    __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, int part) const {
+        const int n = threadIdx.x / KQ, c = (threadIdx.x % KQ) * 4 + part;
+        const uint32_t wd = part == 0 ? raw.x : part == 1 ? raw.y : part == 2 ? raw.z : raw.w;
+        *reinterpret_cast<u32x4_t *>(s + swz_t<BP>(n, c)) = lookup8(tb, wd);
     }
 };
+
+// dX MFMA step: A operand = W^T (rows k) read transposed from the natural-layout tile with
+// ds_read_b64_tr_b16: in each 16-lane group, lane q points at 4 consecutive k of row
+// n0 + q / 4, and lane q then holds W[n0 .. n0+3][k0 + q]; two reads give the 8 n of a
+// 32x32x16 fragment.  B operand = dY tile (rows m) as in the forward kernel.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+__device__ __forceinline__ uint2 tr_read(const uint8_t *s, int off) {
+    const v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16_t *)((__attribute__((address_space(3))) uint8_t *)s + off));
+    return __builtin_bit_cast(uint2, v);
+}
+
+template <int DT, int BP, int TP, int TM, class Part>
+__device__ __forceinline__ void mma_step_dx(float16_t (&acc)[TP][TM], const uint8_t *sw,
+                                            const uint8_t *sa, int prow0, int mrow0, Part &&part) {
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31;
+    const int kh = lane >> 5;
+    const int q = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < BR / 16; ++ks) {
+        u32x4_t fa[TP], fb[TM];
+        const int n0 = ks * 16 + (g >> 1) * 8 + (q >> 2);
+#pragma unroll
+        for (int i = 0; i < TP; ++i) {
+            const int k = prow0 + i * 32 + (g & 1) * 16 + (q & 3) * 4;
+            const uint2 lo = tr_read(sw, swz_t<BP>(n0, k >> 3) + (k & 7) * 2);
+            const uint2 hi = tr_read(sw, swz_t<BP>(n0 + 4, k >> 3) + (k & 7) * 2);
+            fa[i] = (u32x4_t){lo.x, lo.y, hi.x, hi.y};
+        }
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+            fb[j] = *reinterpret_cast<const u32x4_t *>(sa + swz(mrow0 + j * 32 + r, ks * 2 + kh));
+#pragma unroll
+        for (int i = 0; i < TP; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc[i][j] = mfma32<DT>(fa[i], fb[j], acc[i][j]);
+        part(ks);
+    }
+}
 
 // ------------------------------------------------------------------------------- kernels
 
@@ -381,7 +512,6 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     static_assert(NT == 2 * BP, "forward weight tile mapping needs 2 threads per row");
     __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BP * ROWB];
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
-    __shared__ float s_code[16];
     __shared__ float s_code2[256];
 
     const int64_t bid = blockIdx.x;
@@ -391,16 +521,17 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const int64_t local = tile - a.tile_start[seg];
     const int64_t p0 = (local / a.m_tiles) * BP;
     const int64_t m0 = (local % a.m_tiles) * BM;
-    const DevWeight &w = a.w[seg];
+    const DevWeight w = a.w[seg];  // by value: kept in registers for the whole loop
     const int64_t K = a.K;
     const int64_t steps = K / BR;
     const int64_t per = (steps + a.splits - 1) / a.splits;
     const int64_t s0 = split * per;
     const int64_t s1 = s0 + per < steps ? s0 + per : steps;
 
-    for (int i = threadIdx.x; i < 16; i += NT) s_code[i] = w.code[i];
     if (w.nested)
         for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = w.code2[i];
+    float code_r[16];
+    load_code_sgpr(w.code, code_r);
 
     const int wave = threadIdx.x >> 6;
     const int wp = wave % WP, wm = wave / WP;
@@ -442,25 +573,52 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
             for (int j = 0; j < TM; ++j) acc[i][j] *= lo.scale;
     }
 
-    FwdWeight<DT, BP> wt;
+    // Two register stages (steps st+1 and st+2 in flight) and two LDS stages (st and st+1).
+    // Step st computes from LDS stage (st - s0) & 1 while the other LDS stage receives step
+    // st+1 from register stage (st + 1 - s0) & 1, a quarter per MFMA k-substep; the register
+    // stage of st has been consumed, so it takes the global loads of st+2.
+    FwdWeight<DT, BP> wt[2] = {};
+    ActTile<BM, NT> at[2] = {};
     __syncthreads();  // tables
+    const WeightRsrc wr = weight_rsrc(w);
+    const rsrc_t ar = act_rsrc<BM>(a, m0);
     if (s0 < s1) {
-        act_load_direct<BM, NT>(a, sA[0], m0, s0 * BR);
-        wt.load(w, p0, K, s0);
-        wt.store(w, sW[0], s_code, s_code2);
-        __builtin_amdgcn_s_waitcnt(0);
+        at[0].load(ar, a.ld_act, s0 * BR);
+        wt[0].load(wr, p0, K, s0);
+        if (s0 + 1 < s1) {
+            at[1].load(ar, a.ld_act, (s0 + 1) * BR);
+            wt[1].load(wr, p0, K, s0 + 1);
+        }
+        at[0].store(sA[0]);
+        {
+            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, s_code2));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
+        }
         __syncthreads();
-        for (int64_t st = s0; st < s1; ++st) {
-            const int buf = static_cast<int>((st - s0) & 1);
-            const bool more = st + 1 < s1;
-            if (more) {
-                act_load_direct<BM, NT>(a, sA[buf ^ 1], m0, (st + 1) * BR);
-                wt.load(w, p0, K, st + 1);
+        for (int64_t st0 = s0; st0 < s1; st0 += 2) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int64_t st = st0 + b;
+                if (st < s1) {
+                    // On the last step the stores below write a stale stage into the LDS stage
+                    // nobody reads again: unconditional, so they interleave with the MFMAs.
+                    // stage b was drained into LDS during the previous step: refill it first,
+                    // so its loads have a whole step before they are needed
+                    if (st + 2 < s1) {
+                        at[b].load(ar, a.ld_act, (st + 2) * BR);
+                        wt[b].load(wr, p0, K, st + 2);
+                    }
+                    const Nf4Table tb =
+                        make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, s_code2));
+                    mma_step_interleaved<DT, TP, TM>(
+                        acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
+                            at[b ^ 1].store_part(sA[b ^ 1], ks);
+                            wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                        });
+                    __syncthreads();
+                }
             }
-            mma_step<DT, TP, TM>(acc, sW[buf], sA[buf], wp * (BP / WP), wm * (BM / WM));
-            if (more) wt.store(w, sW[buf ^ 1], s_code, s_code2);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
         }
     }
     epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), w.rows, a.seg_off[seg],
@@ -474,7 +632,6 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     static_assert(NT == 2 * BP, "dX weight tile mapping needs 2 threads per k column group");
     __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BP * ROWB];
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
-    __shared__ float s_code[kMaxSeg][16];
     __shared__ float s_code2[kMaxSeg][256];
 
     const int64_t bid = blockIdx.x;
@@ -488,7 +645,6 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     const int64_t s1 = s0 + per < a.total_steps ? s0 + per : a.total_steps;
 
     for (int s = 0; s < a.nseg; ++s) {
-        for (int i = threadIdx.x; i < 16; i += NT) s_code[s][i] = a.w[s].code[i];
         if (a.w[s].nested)
             for (int i = threadIdx.x; i < 256; i += NT) s_code2[s][i] = a.w[s].code2[i];
     }
@@ -532,33 +688,58 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
         }
     }
 
-    DxWeight<DT, BP> wt;
-    // One reduction step: segment seg, rows n0 .. n0+64 of it.
-    auto load_step = [&](int64_t st, uint8_t *sa_buf, int &seg) {
-        seg = seg_of_step(a, st);
-        const int64_t n0 = (st - a.step_start[seg]) * BR;
-        const int64_t rows = a.w[seg].rows;
-        const int64_t col0 = a.seg_off[seg] + n0;
-        if (n0 + BR <= rows) act_load_direct<BM, NT>(a, sa_buf, m0, col0);
-        else act_load_masked<BM, NT>(a, sa_buf, m0, col0, a.seg_off[seg] + rows);
-        wt.load(a.w[seg], n0, p0, K);
-    };
-
+    DxWeight<DT, BP> wt[2] = {};
+    ActTile<BM, NT> at[2] = {};
+    const rsrc_t ar = act_rsrc<BM>(a, m0);
     __syncthreads();  // tables
-    if (s0 < s1) {
-        int seg;
-        load_step(s0, sA[0], seg);
-        wt.store(a.w[seg], sW[0], s_code[seg], s_code2[seg]);
-        __builtin_amdgcn_s_waitcnt(0);
+    // The reduction range [s0, s1) walks the stacked segments in order; each segment runs the
+    // forward kernel's pipeline (two register stages, two LDS stages, next tile's staging
+    // interleaved with the MFMAs) with its descriptor held in registers.
+    for (int seg = seg_of_step(a, s0); seg < a.nseg && a.step_start[seg] < s1; ++seg) {
+        const int64_t b0 = a.step_start[seg] > s0 ? a.step_start[seg] : s0;
+        const int64_t e0 = a.step_start[seg + 1] < s1 ? a.step_start[seg + 1] : s1;
+        if (b0 >= e0) continue;
+        const DevWeight w = a.w[seg];
+        const WeightRsrc wr = weight_rsrc(w);
+        const int64_t col_base = a.seg_off[seg];
+        const int64_t col_end = col_base + w.rows;
+        const int64_t first = a.step_start[seg];
+        const float *code2 = s_code2[seg];
+        float code_r[16];
+        load_code_sgpr(w.code, code_r);
+        // Stage step st into register stage x; a segment's partial last step (rows % 64 != 0)
+        // has its columns past the segment zeroed (uniform branch, at most once per segment).
+        auto stage = [&](ActTile<BM, NT> &t, DxWeight<DT, BP> &u, int64_t st) {
+            const int64_t col0 = col_base + (st - first) * BR;
+            t.load(ar, a.ld_act, col0);
+            if (col0 + BR > col_end) t.mask(col0, col_end);
+            u.load(wr, (st - first) * BR, p0, K);
+        };
+        stage(at[0], wt[0], b0);
+        if (b0 + 1 < e0) stage(at[1], wt[1], b0 + 1);
+        at[0].store(sA[0]);
+        {
+            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
+        }
         __syncthreads();
-        for (int64_t st = s0; st < s1; ++st) {
-            const int buf = static_cast<int>((st - s0) & 1);
-            const bool more = st + 1 < s1;
-            if (more) load_step(st + 1, sA[buf ^ 1], seg);
-            mma_step<DT, TP, TM>(acc, sW[buf], sA[buf], wp * (BP / WP), wm * (BM / WM));
-            if (more) wt.store(a.w[seg], sW[buf ^ 1], s_code[seg], s_code2[seg]);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+        for (int64_t st0 = b0; st0 < e0; st0 += 2) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int64_t st = st0 + b;
+                if (st < e0) {
+                    if (st + 2 < e0) stage(at[b], wt[b], st + 2);
+                    const Nf4Table tb =
+                        make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
+                    mma_step_dx<DT, BP, TP, TM>(
+                        acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
+                            at[b ^ 1].store_part(sA[b ^ 1], ks);
+                            wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                        });
+                    __syncthreads();
+                }
+            }
         }
     }
     epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), K, 0, m0 + wm * (BM / WM), split);
@@ -607,31 +788,48 @@ int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const n
         const int st = check_weight(&ws[i]);
         if (st != NF4_OK) return st;
         if (ws[i].cols != g.K) return NF4_ERR_ARG;
-        // The fused main loop needs each 64-wide step of a weight row inside one absmax block.
+        // The fused main loop needs each 64-wide step of a weight row inside one absmax block,
+        // and power-of-two block sizes (shifts instead of divisions in the main loop).
         if (ws[i].blocksize % BR != 0 || g.K % ws[i].blocksize != 0) return NF4_ERR_UNSUPPORTED;
+        if (log2_exact(ws[i].blocksize) < 0) return NF4_ERR_UNSUPPORTED;
+        if (ws[i].nested && log2_exact(ws[i].blocksize2) < 0) return NF4_ERR_UNSUPPORTED;
         if (!aligned(ws[i].packed, 16)) return NF4_ERR_UNSUPPORTED;
         g.w[i] = to_dev(ws[i]);
     }
     if (g.K % BR != 0 || ld_act % 8 != 0 || !aligned(act, 16)) return NF4_ERR_UNSUPPORTED;
+    // Main-loop loads use 32-bit byte offsets inside buffer resources: a 256-row activation
+    // window and each weight (plus one tile of rows past its end) must stay below 2 GiB.
+    if (ld_act >= (int64_t(1) << 21)) return NF4_ERR_UNSUPPORTED;
+    for (int i = 0; i < nw; ++i) {
+        const int64_t n = (ws[i].rows + 256) * ws[i].cols;
+        if (n / 2 >= (int64_t(1) << 31) || (n / ws[i].blocksize) * 4 >= (int64_t(1) << 31))
+            return NF4_ERR_UNSUPPORTED;
+    }
     return NF4_OK;
 }
 
-// Splits of the reduction so that about one round of workgroups covers the GPU, keeping at
-// least 8 steps per split.
-int choose_splits(int64_t tiles, int64_t steps, int per_cu) {
-    int s = 1;
-    while (tiles * s * 2 <= kCUs * per_cu && steps / (s * 2) >= 8 && s < 16) s *= 2;
-    return s;
+// Tile choice.  The 256x256 tile (8 waves) keeps VALU dequant work under the MFMA time (it is
+// spread over 256 rows of activations); the 128x128 tile (4 waves, 2 workgroups per CU) is VALU-
+// bound and only used when the big tiles cannot fill half of the GPU even with split-K.  The
+// reduction is split into at most kCUs / tiles parts of at least kMinSteps steps each.
+constexpr int kMinSteps = 6;
+
+int splits_for(int64_t tiles, int64_t steps, int per_cu) {
+    int64_t s = (kCUs * per_cu) / (tiles > 0 ? tiles : 1);
+    const int64_t by_steps = steps / kMinSteps;
+    if (s > by_steps) s = by_steps;
+    if (s > 16) s = 16;
+    return s < 1 ? 1 : static_cast<int>(s);
 }
 
 Plan make_plan(int64_t big, int64_t small, int64_t steps) {
     Plan p{};
-    if (big >= kCUs) {
-        p.cfg = 0; p.bp = 256; p.bm = 256; p.tiles = big;
-        p.splits = choose_splits(big, steps, 1);
+    const int sb = big >= kCUs ? 1 : splits_for(big, steps, 1);
+    if (big * sb >= kCUs / 2) {
+        p.cfg = 0; p.bp = 256; p.bm = 256; p.tiles = big; p.splits = sb;
     } else {
         p.cfg = 1; p.bp = 128; p.bm = 128; p.tiles = small;
-        p.splits = choose_splits(small, steps, 2);
+        p.splits = small >= 2 * kCUs ? 1 : splits_for(small, steps, 2);
     }
     return p;
 }
@@ -722,6 +920,7 @@ extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_w
         n_out += ws[i].rows;
     }
     if (ldy < n_out) return NF4_ERR_ARG;
+    g.act_cols = g.K;
     for (int i = 0; i < nlora; ++i) {
         const nf4_lora &l = loras[i];
         if (l.seg < 0 || l.seg >= nw || l.rank < 1 || l.rank > 64 || !l.t || !l.b) return NF4_ERR_ARG;
@@ -775,6 +974,7 @@ extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_
         n_in += ws[i].rows;
     }
     if (lddy < n_in || lddx < g.K) return NF4_ERR_ARG;
+    g.act_cols = n_in;
     for (int i = 0; i < nlora; ++i) {
         const nf4_lora &l = loras[i];
         if (l.seg < 0 || l.seg >= nw || l.rank < 1 || l.rank > 64 || !l.a || !l.da) return NF4_ERR_ARG;

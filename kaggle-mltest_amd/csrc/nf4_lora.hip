@@ -23,94 +23,135 @@ __device__ __forceinline__ uint16_t st1(float v) {
 }
 
 template <int DT>
-__device__ __forceinline__ void unpack8(const u32x4_t &v, float (&f)[8]) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint16_t lo = w[i] & 0xffff, hi = w[i] >> 16;
-        f[2 * i] = ld1<DT>(&lo);
-        f[2 * i + 1] = ld1<DT>(&hi);
+__device__ __forceinline__ float4_t mfma16(const u32x4_t &a, const u32x4_t &b, const float4_t &c) {
+    if constexpr (DT == NF4_BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf168_t, a),
+                                                      __builtin_bit_cast(bf168_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                     __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
     }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
+// 8 16-bit values src[j * stride], j < lim (the rest zero), as an MFMA fragment; one 16-byte
+// load when the 8 are contiguous, in range and aligned.
+__device__ __forceinline__ u32x4_t frag8(const uint16_t *src, int64_t stride, int lim, bool vec) {
+    if (vec && stride == 1 && lim >= 8) return *reinterpret_cast<const u32x4_t *>(src);
+    uint16_t e[8];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    for (int j = 0; j < 8; ++j) e[j] = (j < lim) ? src[j * stride] : 0;
+    u32x4_t v;
+    v.x = e[0] | (uint32_t(e[1]) << 16);
+    v.y = e[2] | (uint32_t(e[3]) << 16);
+    v.z = e[4] | (uint32_t(e[5]) << 16);
+    v.w = e[6] | (uint32_t(e[7]) << 16);
     return v;
 }
 
 constexpr int kMaxRank = 64;
 
-// t[m][j] = sum_k xd[m][k] * A[j][k].  One wave per row m; lanes stride k by 8 elements.
-// Also serves da[m][j] = scale * sum_n dY[m][n] * B[n][j] with `a_rowmajor_rank` = true
-// (B is [N, rank]: the rank index is contiguous).
+// out[m][j] = scale * sum_k act[m][k] * W(j, k) on v_mfma_f32_16x16x32, where
+//   W(j, k) = w[j * K + k]    (B_LAYOUT false: LoRA A [rank, K], for t = xd A^T)
+//   W(j, k) = w[k * rank + j] (B_LAYOUT true:  LoRA B [N, rank], for da = s dY B).
+// A workgroup owns 16 rows m; its 4 waves split the reduction and add their 16 x 16 partial
+// tiles through LDS in a fixed order.  MFMA A operand = W (rows j), B operand = act (cols m).
 template <int DT, bool B_LAYOUT>
 __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t *act, int64_t m, int64_t k,
                                                      int64_t ld, const uint16_t *w, int rank,
-                                                     float scale, uint16_t *out) {
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= m) return;
+                                                     float scale, uint16_t *out, int vec) {
+    __shared__ float4_t red[4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t kc = ((k + 127) / 128) * 32;  // per-wave share of k, a multiple of 32
+    const int64_t kb = wave * kc;
+    const int64_t ke = kb + kc < k ? kb + kc : k;
+    const int col = lane & 15, kq = (lane >> 4) * 8;
+    const int64_t row = m0 + col;
     for (int j0 = 0; j0 < rank; j0 += 16) {
-        float acc[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[j] = 0.f;
-        const int jn = rank - j0 < 16 ? rank - j0 : 16;
-        for (int64_t c = lane * 8; c < k; c += 512) {
-            float x[8];
-            if (c + 8 <= k) {
-                unpack8<DT>(*reinterpret_cast<const u32x4_t *>(act + row * ld + c), x);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = c + e < k ? ld1<DT>(act + row * ld + c + e) : 0.f;
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+        const int j = j0 + col;
+        for (int64_t k0 = kb; k0 < ke; k0 += 32) {
+            const int64_t kk = k0 + kq;
+            const int lim = ke - kk < 8 ? static_cast<int>(ke - kk) : 8;
+            u32x4_t fa = {0u, 0u, 0u, 0u}, fb = {0u, 0u, 0u, 0u};
+            if (lim > 0) {
+                if (j < rank)
+                    fa = B_LAYOUT ? frag8(w + kk * rank + j, rank, lim, false)
+                                  : frag8(w + j * k + kk, 1, lim, (vec & 2) != 0);
+                if (row < m) fb = frag8(act + row * ld + kk, 1, lim, (vec & 1) != 0);
             }
+            acc = mfma16<DT>(fa, fb, acc);
+        }
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            const float4_t s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+            const int64_t mm = m0 + (lane & 15);
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                if (j >= jn) break;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    if (c + e < k) {
-                        const uint16_t *wp = B_LAYOUT ? w + (c + e) * rank + j0 + j
-                                                      : w + (j0 + j) * k + c + e;
-                        acc[j] = fmaf(x[e], ld1<DT>(wp), acc[j]);
-                    }
-                }
+            for (int q = 0; q < 4; ++q) {
+                const int jj = j0 + (lane >> 4) * 4 + q;
+                if (mm < m && jj < rank) out[mm * rank + jj] = st1<DT>(s[q] * scale);
             }
         }
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            if (j >= jn) break;
-            const float s = wave_sum(acc[j]);
-            if (lane == 0) out[row * rank + j0 + j] = st1<DT>(s * scale);
-        }
+        __syncthreads();
     }
 }
 
-// Partial sums over a chunk of rows: part[chunk][p][j] = sum_{m in chunk} U[m][p] * V[m][j].
+// Partial sums over a chunk of rows on v_mfma_f32_16x16x32:
+//   part[chunk][p][j] = sum_{m in chunk} U[m][p] * V[m][j]
+// for a 64-column tile of p (4 waves x 16) and one 16-wide tile of j (blockIdx.z).  Both
+// operands are reduced over m, so each 32-row step is staged in LDS transposed ([p][m], [j][m])
+// and the MFMA fragments are contiguous 16-byte LDS reads.
 template <int DT>
 __global__ __launch_bounds__(256) void wgrad_partial_kernel(const uint16_t *u, int64_t m, int64_t p,
                                                             int64_t ldu, const uint16_t *v, int rank,
-                                                            int64_t rows_per_chunk, float *part) {
-    const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+                                                            int64_t rows_per_chunk, float *part,
+                                                            int vec_u) {
+    constexpr int SR = 40;  // LDS row: 32 m + 8 pad (80 bytes)
+    __shared__ __attribute__((aligned(16))) uint16_t sU[64 * SR];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[16 * SR];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 64;
     const int64_t chunk = blockIdx.y;
+    const int j0 = blockIdx.z * 16;
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
-    for (int j0 = 0; j0 < rank; j0 += 16) {
-        const int jn = rank - j0 < 16 ? rank - j0 : 16;
-        float acc[16];
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t mb = r0; mb < r1; mb += 32) {
+        {   // U[mb .. mb+32][p0 .. p0+64] -> sU[p][m]
+            const int rr = threadIdx.x >> 3, pc = (threadIdx.x & 7) * 8;
+            const int64_t mm = mb + rr, pp = p0 + pc;
+            const int lim = (mm < r1) ? (p - pp < 8 ? static_cast<int>(p - pp) : 8) : 0;
+            const u32x4_t x = lim > 0 ? frag8(u + mm * ldu + pp, 1, lim, vec_u != 0)
+                                      : (u32x4_t){0u, 0u, 0u, 0u};
+            const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[j] = 0.f;
-        if (col < p) {
-            for (int64_t r = r0; r < r1; ++r) {
-                const float x = ld1<DT>(u + r * ldu + col);
-#pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    if (j < jn) acc[j] = fmaf(x, ld1<DT>(v + r * rank + j0 + j), acc[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (j < jn) part[(chunk * p + col) * rank + j0 + j] = acc[j];
+            for (int q = 0; q < 8; ++q)
+                sU[(pc + q) * SR + rr] = static_cast<uint16_t>(xw[q >> 1] >> ((q & 1) * 16));
         }
+        if (threadIdx.x < 64) {  // V[mb .. mb+32][j0 .. j0+16] -> sV[j][m]
+            const int rr = threadIdx.x >> 1, jc = (threadIdx.x & 1) * 8;
+            const int64_t mm = mb + rr;
+            const int lim = (mm < r1) ? (rank - (j0 + jc) < 8 ? rank - (j0 + jc) : 8) : 0;
+            const u32x4_t x = lim > 0 ? frag8(v + mm * rank + j0 + jc, 1, lim, false)
+                                      : (u32x4_t){0u, 0u, 0u, 0u};
+            const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                sV[(jc + q) * SR + rr] = static_cast<uint16_t>(xw[q >> 1] >> ((q & 1) * 16));
+        }
+        __syncthreads();
+        const u32x4_t fa = *reinterpret_cast<const u32x4_t *>(sU + (wave * 16 + (lane & 15)) * SR +
+                                                              (lane >> 4) * 8);
+        const u32x4_t fb = *reinterpret_cast<const u32x4_t *>(sV + (lane & 15) * SR + (lane >> 4) * 8);
+        acc = mfma16<DT>(fa, fb, acc);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t pp = p0 + wave * 16 + (lane >> 4) * 4 + q;
+        const int jj = j0 + (lane & 15);
+        if (pp < p && jj < rank) part[(chunk * p + pp) * rank + jj] = acc[q];
     }
 }
 
@@ -186,7 +227,16 @@ int grid_for(int64_t n) {
     return static_cast<int>(b > 16384 ? 16384 : (b < 1 ? 1 : b));
 }
 
-constexpr int64_t kRowsPerChunk = 64;
+// Rows of M per wgrad workgroup: about 512 workgroups over the (64-column p tile x chunk) grid,
+// in multiples of the 32-row step.
+int64_t wgrad_rows_per_chunk(int64_t m, int64_t p) {
+    const int64_t p_tiles = (p + 63) / 64;
+    int64_t chunks = 512 / p_tiles;
+    if (chunks < 1) chunks = 1;
+    int64_t rows = (m + chunks - 1) / chunks;
+    rows = ((rows + 31) / 32) * 32;
+    return rows < 32 ? 32 : rows;
+}
 
 }  // namespace
 
@@ -209,16 +259,19 @@ extern "C" int nf4_lora_xa(const void *xd, int64_t m, int64_t k, int64_t ldx, co
         return NF4_ERR_ARG;
     if (m == 0) return NF4_OK;
     if (!xd || !a || !t || ldx < k) return NF4_ERR_ARG;
-    if (ldx % 8 || !aligned(xd, 16)) return NF4_ERR_UNSUPPORTED;
-    const dim3 grid(static_cast<unsigned>((m + 3) / 4));
+    if ((m + 15) / 16 > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
+    const dim3 grid(static_cast<unsigned>((m + 15) / 16));
+    const int vec = (ldx % 8 == 0 && aligned(xd, 16) ? 1 : 0) | (k % 8 == 0 && aligned(a, 16) ? 2 : 0);
     auto s = static_cast<hipStream_t>(stream);
     auto A = static_cast<const uint16_t *>(xd);
     if (dtype == NF4_BF16)
         hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, false>), grid, dim3(256), 0, s, A, m, k, ldx,
-                           static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t));
+                           static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t),
+                           vec);
     else
         hipLaunchKernelGGL((rowdot_kernel<NF4_F16, false>), grid, dim3(256), 0, s, A, m, k, ldx,
-                           static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t));
+                           static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t),
+                           vec);
     return status_of(hipGetLastError());
 }
 
@@ -228,22 +281,26 @@ extern "C" int nf4_lora_da(const void *dy, int64_t m, int64_t n, int64_t lddy, c
         return NF4_ERR_ARG;
     if (m == 0) return NF4_OK;
     if (!dy || !b || !da || lddy < n) return NF4_ERR_ARG;
-    if (lddy % 8 || !aligned(dy, 16)) return NF4_ERR_UNSUPPORTED;
-    const dim3 grid(static_cast<unsigned>((m + 3) / 4));
+    if ((m + 15) / 16 > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
+    const dim3 grid(static_cast<unsigned>((m + 15) / 16));
+    const int vec = lddy % 8 == 0 && aligned(dy, 16) ? 1 : 0;
     auto s = static_cast<hipStream_t>(stream);
     auto A = static_cast<const uint16_t *>(dy);
     if (dtype == NF4_BF16)
         hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, true>), grid, dim3(256), 0, s, A, m, n, lddy,
-                           static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da));
+                           static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da),
+                           vec);
     else
         hipLaunchKernelGGL((rowdot_kernel<NF4_F16, true>), grid, dim3(256), 0, s, A, m, n, lddy,
-                           static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da));
+                           static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da),
+                           vec);
     return status_of(hipGetLastError());
 }
 
 extern "C" size_t nf4_lora_wgrad_workspace(int64_t m, int64_t p, int rank) {
     if (m <= 0 || p <= 0 || rank <= 0) return 0;
-    const int64_t chunks = (m + kRowsPerChunk - 1) / kRowsPerChunk;
+    const int64_t rows = wgrad_rows_per_chunk(m, p);
+    const int64_t chunks = (m + rows - 1) / rows;
     return static_cast<size_t>(chunks) * p * rank * sizeof(float);
 }
 
@@ -261,18 +318,21 @@ extern "C" int nf4_lora_wgrad(const void *u, int64_t m, int64_t p, int64_t ldu, 
     }
     const size_t need = nf4_lora_wgrad_workspace(m, p, rank);
     if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
-    const int64_t chunks = (m + kRowsPerChunk - 1) / kRowsPerChunk;
-    if (chunks > 65535) return NF4_ERR_UNSUPPORTED;
+    const int64_t rows = wgrad_rows_per_chunk(m, p);
+    const int64_t chunks = (m + rows - 1) / rows;
+    if (chunks > 65535 || (p + 63) / 64 > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
     float *part = static_cast<float *>(workspace);
-    const dim3 grid(static_cast<unsigned>((p + 255) / 256), static_cast<unsigned>(chunks));
+    const dim3 grid(static_cast<unsigned>((p + 63) / 64), static_cast<unsigned>(chunks),
+                    static_cast<unsigned>((rank + 15) / 16));
+    const int vec_u = ldu % 8 == 0 && aligned(u, 16) ? 1 : 0;
     if (dtype == NF4_BF16)
         hipLaunchKernelGGL(wgrad_partial_kernel<NF4_BF16>, grid, dim3(256), 0, s,
                            static_cast<const uint16_t *>(u), m, p, ldu,
-                           static_cast<const uint16_t *>(v), rank, kRowsPerChunk, part);
+                           static_cast<const uint16_t *>(v), rank, rows, part, vec_u);
     else
         hipLaunchKernelGGL(wgrad_partial_kernel<NF4_F16>, grid, dim3(256), 0, s,
                            static_cast<const uint16_t *>(u), m, p, ldu,
-                           static_cast<const uint16_t *>(v), rank, kRowsPerChunk, part);
+                           static_cast<const uint16_t *>(v), rank, rows, part, vec_u);
     int st = status_of(hipGetLastError());
     if (st != NF4_OK) return st;
     hipLaunchKernelGGL(wgrad_final_kernel, dim3(static_cast<unsigned>((p * rank + 255) / 256)),

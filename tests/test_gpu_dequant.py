@@ -59,7 +59,8 @@ def test_reference_shapes_bit_exact(cuda, shape):
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("nested", [True, False])
 @pytest.mark.parametrize("shape,bs", [((7, 9), 64), ((33, 64), 32), ((100, 384), 128),
-                                      ((3, 1000), 256), ((5, 6), 2), ((64, 192), 64)])
+                                      ((3, 1000), 256), ((5, 6), 2), ((64, 192), 64),
+                                      ((12, 40), 8), ((9, 30), 16)])
 def test_layouts_bit_exact(cuda, dt, nested, shape, bs):
     from solution.nf4 import dequantize_nf4
 

@@ -39,6 +39,27 @@ def test_fixture_forward_and_dx(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape,bs,nested", [((384, 256), 64, True), ((256, 1536), 64, True),
+                                             ((200, 512), 128, True), ((136, 320), 64, False)])
+def test_fused_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
+    """With X = I the forward GEMM returns W^T and with dY = I the input gradient returns W,
+    each output one exact product: the weight dequantized inside the GEMM main loop must equal
+    the oracle's bit for bit."""
+    from solution import kernels
+
+    n, k = shape
+    banner("fused dequant exact", shape, bs, nested, dtype)
+    p, qs = random_weight(n, k, seed=n + k, dev=cuda, blocksize=bs, nested=nested)
+    ref = oracle_w16(p, qs, "bf16" if dtype == torch.bfloat16 else "f16").view(torch.int16)
+    eye_k = torch.eye(k, dtype=dtype, device=cuda)
+    y = kernels.linear_fwd(eye_k, [(p, qs)])
+    assert torch.equal(y.t().contiguous().cpu().view(torch.int16), ref)
+    eye_n = torch.eye(n, dtype=dtype, device=cuda)
+    dx = kernels.linear_dx(eye_n, [(p, qs)])
+    assert torch.equal(dx.cpu().view(torch.int16), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("proj", list(QWEN_15B))
 def test_qwen_projection_m2048(cuda, proj, dtype):
     from solution import kernels
