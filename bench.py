@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dequant", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after timing, copy this many MiB device-to-device 3 times: the "
+                         "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -361,6 +364,21 @@ def cpu_baseline(dtype_name, reps):
 
 # ------------------------------------------------------------------------------------- main
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_traffic_m2048.md"
+
+
+def measured_traffic(kernel: str, dtype_name: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (fp16 runs, calibrated against a device copy of known size), or None."""
+    if dtype_name != "f16" or not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            vals = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
+            return int(vals[kernel]) if kernel in vals else None
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -410,7 +428,8 @@ def main():
         "mfma_peak_frac": round(value / PEAK_MFMA_TFLOPS, 4),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_MFMA_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
+                     "traffic": measured_traffic(dom, args.dtype),
                      "us_per_launch": round(per[dom] * 1e3, 2),
                      "gflop_per_launch": round(gf[dom] / 1e9, 3)},
         "gemm_us_per_launch": {n: round(v * 1e3, 2) for n, v in per.items()},
@@ -423,6 +442,13 @@ def main():
         out["dequant"] = dict(dq, roofline={"bound": "hbm", "achieved": dq["gbps"],
                                             "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                             "frac": dq["frac"], "traffic": None})
+    if args.copy_mib > 0:
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_calibration_bytes"] = src.numel()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.dtype, args.cpu_reps)
     print(json.dumps(out), flush=True)

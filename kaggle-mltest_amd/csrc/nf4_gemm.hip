@@ -13,19 +13,21 @@
 // With v_mfma_f32_32x32x16 each lane then owns one activation row m and four consecutive p,
 // so results leave as 8-byte row-major stores of Y[m, n..n+3] or dX[m, k..k+3].
 //
-// Workgroup tile BP x BM, reduction step 64 (one NF4 absmax block along k for the forward
-// weight), two LDS stages.  LDS tiles are rows of 64 16-bit values (128 bytes) whose 16-byte
-// chunks are XOR-swizzled by the row index, so MFMA fragment reads of 32 consecutive rows spread
-// over the banks.  Per step:
-//   * the activation tile of the next step streams straight from global memory into the other
-//     LDS stage (global_load_lds_dwordx4, no registers; lanes pick their global chunk so that
-//     the lane-linear LDS writes land in the swizzled layout);
-//   * the packed weight bytes of the next step (4x smaller than fp16) are prefetched into
-//     registers;
-//   * the MFMAs of the current step run; meanwhile the other wave on the same SIMD dequantizes
-//     (NF4 table in LDS, absmax rebuilt from its uint8 code, fp32 product, one RNE conversion)
-//     and writes the next weight tile to LDS;
+// Workgroup tile BP x BM (256x256 with 8 waves, or 128x128 with 4), reduction step 64 (one NF4
+// absmax block along k for the forward weight), two LDS stages and two register stages.  LDS
+// tiles are rows of 64 16-bit values (128 bytes) whose 16-byte chunks are XOR-swizzled with bits
+// 1..3 of the row, so the 16 rows one 16-lane group of an MFMA fragment read hit distinct banks.
+// Per step s:
+//   * activations and packed weight bytes of step s + 2 are loaded into registers through
+//     buffer resources (hardware range checks return 0 past the end: no branches, so the
+//     compiler's wait counts stay exact);
+//   * the MFMAs of step s run in four k-substeps; after each substep a quarter of step s + 1's
+//     staging runs: activation chunks to LDS, weight nibbles dequantized by a register table
+//     (v_perm_b32 byte selects over the 16 values round(code[i] * absmax), absmax rebuilt from
+//     its uint8 code) and written to LDS;
 //   * one barrier.
+// The dX weight tile keeps W's natural [n][k] layout; the MFMA A operand (rows k) is read
+// transposed out of it with ds_read_b64_tr_b16.
 // Long reductions are split over workgroups into fp32 partial sums that a reduction kernel
 // adds up in a fixed order (deterministic).
 

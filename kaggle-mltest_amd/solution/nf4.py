@@ -99,9 +99,16 @@ def _nf4_state_ok(packed, quant_state, in_features):
 
 def _fused_ok(quant_state) -> bool:
     """The layouts the fused GEMM covers: each 64-wide step of a weight row inside one absmax
-    block (blocksize a multiple of 64 dividing in_features)."""
+    block (a power-of-two blocksize >= 64 dividing in_features; a power-of-two double-quant
+    group when nested).  bitsandbytes writes powers of two only."""
     bs, k = int(quant_state.blocksize), int(quant_state.shape[1])
-    return bs % 64 == 0 and k % bs == 0
+    if bs < 64 or bs & (bs - 1) or k % bs:
+        return False
+    inner = getattr(quant_state, "state2", None)
+    if getattr(quant_state, "nested", False) and inner is not None:
+        bs2 = int(inner.blocksize)
+        return bs2 > 0 and not bs2 & (bs2 - 1)
+    return True
 
 
 def _supported(x, packed, quant_state):
