@@ -103,18 +103,6 @@ __device__ __forceinline__ uint16_t from_f32(float v) {
     else return __builtin_bit_cast(uint16_t, static_cast<half_t>(v));
 }
 
-// 8 NF4 codes of one dword (byte j: high nibble = element 2j, low = 2j+1) times absmax,
-// rounded once to DT and packed.
-template <int DT>
-__device__ __forceinline__ u32x4_t dequant8(uint32_t p, float s, const float *code) {
-    u32x4_t r;
-    r.x = pack2<DT>(__fmul_rn(code[(p >> 4) & 0xF], s), __fmul_rn(code[p & 0xF], s));
-    r.y = pack2<DT>(__fmul_rn(code[(p >> 12) & 0xF], s), __fmul_rn(code[(p >> 8) & 0xF], s));
-    r.z = pack2<DT>(__fmul_rn(code[(p >> 20) & 0xF], s), __fmul_rn(code[(p >> 16) & 0xF], s));
-    r.w = pack2<DT>(__fmul_rn(code[(p >> 28) & 0xF], s), __fmul_rn(code[(p >> 24) & 0xF], s));
-    return r;
-}
-
 __device__ __forceinline__ int seg_of_tile(const GemmArgs &a, int64_t t) {
     int s = 0;
 #pragma unroll
@@ -195,52 +183,57 @@ __device__ __forceinline__ WeightRsrc weight_rsrc(const DevWeight &w) {
 }
 
 // The absmax inputs of block b: uint8 code + absmax2 scale (nested) or the fp32 absmax.
-__device__ __forceinline__ AbsIn absmax_bload(const WeightRsrc &r, int64_t b) {
+__device__ __forceinline__ AbsIn absmax_bload(const WeightRsrc &r, int b) {
     AbsIn a;
-    a.q = bload1(r.q, static_cast<int>(b));
-    const int64_t si = r.nested ? (b >> r.bs2_shift) : b;
-    a.s = __builtin_bit_cast(float, bload4(r.s, static_cast<int>(si * 4)));
+    a.q = bload1(r.q, b);
+    const int si = r.nested ? (b >> r.bs2_shift) : b;
+    a.s = __builtin_bit_cast(float, bload4(r.s, si * 4));
     return a;
 }
 
 // ------------------------------------------------------------------ activation tile loader
 
+// Per-thread byte offsets of an activation tile inside its window: thread t loads chunk t % 8
+// (8 elements) of rows t / 8, t / 8 + NT / 8, ...; a step adds its column offset.  32-bit:
+// the window is below 2 GiB.
+struct ActAddr {
+    int base;   // row t / 8, chunk t % 8
+    int rstep;  // bytes between the rows one thread loads
+};
+
+template <int NT>
+__device__ __forceinline__ ActAddr act_addr(int64_t ld) {
+    ActAddr r;
+    r.base = static_cast<int>(((threadIdx.x >> 3) * ld + (threadIdx.x & 7) * 8) * 2);
+    r.rstep = static_cast<int>((NT / 8) * ld * 2);
+    return r;
+}
+
 // BM rows x 64 columns of act[m][col0 ..] staged through registers: load() issues the global
 // loads of a step (16 bytes per chunk, 8 consecutive threads per 128-byte row), store() writes
 // them to an LDS tile after the current step's MFMAs, so the wait for the loads lands there.
-// Rows >= M and columns >= col_end read as zero.
+// Rows >= M read as zero.
 template <int BM, int NT>
 struct ActTile {
     static constexpr int CH = BM * 8 / NT;
     static_assert(CH >= 1 && BM * 8 % NT == 0, "tile rows must split evenly over the threads");
     u32x4_t r[CH];
 
-    // `rs` covers rows m0 .. min(M, m0 + BM) of the operand (row stride ld elements); rows past
-    // M come back as zero from the hardware range check.
-    __device__ __forceinline__ void load(rsrc_t rs, int64_t ld, int64_t col0) {
+    __device__ __forceinline__ void load(rsrc_t rs, const ActAddr &ad, int col_bytes) {
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int idx = i * NT + threadIdx.x;
-            const int64_t off = (static_cast<int64_t>(idx >> 3) * ld + col0 + (idx & 7) * 8) * 2;
-            r[i] = bload16(rs, static_cast<int>(off));
-        }
+        for (int i = 0; i < CH; ++i) r[i] = bload16(rs, ad.base + i * ad.rstep + col_bytes);
     }
 
-    // Zero the elements at columns >= col_end (a segment's last, partial reduction step).
-    __device__ __forceinline__ void mask(int64_t col0, int64_t col_end) {
+    // Zero the elements at columns >= valid of the step (a segment's partial last step).
+    __device__ __forceinline__ void mask(int valid) {
+        const int k = valid - static_cast<int>(threadIdx.x & 7) * 8;  // valid elements of my chunks
+        uint32_t mk[4];
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int idx = i * NT + threadIdx.x;
-            const int64_t k = col_end - (col0 + (idx & 7) * 8);  // valid elements of the chunk
-            uint32_t w[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+        for (int d = 0; d < 4; ++d)
+            mk[d] = ((2 * d < k) ? 0x0000ffffu : 0u) | ((2 * d + 1 < k) ? 0xffff0000u : 0u);
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const uint32_t lo = (2 * d < k) ? 0x0000ffffu : 0u;
-                const uint32_t hi = (2 * d + 1 < k) ? 0xffff0000u : 0u;
-                w[d] &= lo | hi;
-            }
-            r[i] = (u32x4_t){w[0], w[1], w[2], w[3]};
-        }
+        for (int i = 0; i < CH; ++i)
+            r[i] = (u32x4_t){r[i].x & mk[0], r[i].y & mk[1], r[i].z & mk[2], r[i].w & mk[3]};
     }
 
     __device__ __forceinline__ void store(uint8_t *s) const {
@@ -401,27 +394,31 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
 // ------------------------------------------------------------------------ weight tiles
 
 // Forward weight tile: BP rows x 64 k of W (natural layout).  Thread t owns 16 packed bytes =
-// 32 elements of row t/2 (one absmax); NT == 2 * BP.
+// 32 elements of row t/2 (one absmax); NT == 2 * BP.  Offsets are 32-bit: a weight with one
+// tile of rows past its end stays below 2 GiB (checked on the host).
+struct WAddr {
+    int packed;  // byte offset of this thread's 16 packed bytes at step 0
+    int block;   // absmax block of this thread's row at step 0
+};
+
+template <int BP>
+__device__ __forceinline__ WAddr fwd_waddr(const WeightRsrc &r, int64_t p0, int64_t K) {
+    const int64_t row = p0 + (threadIdx.x >> 1);
+    WAddr a;
+    a.packed = static_cast<int>(row * (K >> 1) + (threadIdx.x & 1) * 16);
+    a.block = static_cast<int>(row * (K >> r.bs_shift));
+    return a;
+}
+
 template <int DT, int BP>
 struct FwdWeight {
     u32x4_t raw;
     AbsIn abs;
 
     // Rows past the weight read as zero (their outputs are never stored).
-    __device__ __forceinline__ void load(const WeightRsrc &r, int64_t p0, int64_t K, int64_t st) {
-        const int64_t e0 = (p0 + (threadIdx.x >> 1)) * K + st * BR;
-        raw = bload16(r.packed, static_cast<int>((e0 >> 1) + (threadIdx.x & 1) * 16));
-        abs = absmax_bload(r, e0 >> r.bs_shift);
-    }
-
-    __device__ __forceinline__ void store(const DevWeight &w, uint8_t *s, const float *code,
-                                          const float *code2) const {
-        const int row = threadIdx.x >> 1, h = (threadIdx.x & 1) * 4;
-        const float sc = absmax_val(w, abs, code2);
-        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 0)) = dequant8<DT>(raw.x, sc, code);
-        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 1)) = dequant8<DT>(raw.y, sc, code);
-        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 2)) = dequant8<DT>(raw.z, sc, code);
-        *reinterpret_cast<u32x4_t *>(s + swz(row, h + 3)) = dequant8<DT>(raw.w, sc, code);
+    __device__ __forceinline__ void load(const WeightRsrc &r, const WAddr &ad, int64_t st) {
+        raw = bload16(r.packed, ad.packed + static_cast<int>(st) * (BR / 2));
+        abs = absmax_bload(r, ad.block + static_cast<int>((st * BR) >> r.bs_shift));
     }
 
     // Dword `part` of the 16 packed bytes (8 elements) through the register table of this
@@ -442,18 +439,27 @@ __device__ __forceinline__ int swz_t(int n, int c) {
     return n * (BP * 2) + ((c ^ ((n & 3) << 2)) << 4);
 }
 
+template <int BP>
+__device__ __forceinline__ WAddr dx_waddr(const WeightRsrc &r, int64_t p0, int64_t K) {
+    constexpr int KQ = BP / 32;
+    const int64_t n = threadIdx.x / KQ, k = p0 + (threadIdx.x % KQ) * 32;
+    WAddr a;
+    a.packed = static_cast<int>((n * K + k) >> 1);
+    a.block = static_cast<int>(n * (K >> r.bs_shift) + (k >> r.bs_shift));
+    return a;
+}
+
 template <int DT, int BP>
 struct DxWeight {
     static constexpr int KQ = BP / 32;   // threads per tile row
     u32x4_t raw;
     AbsIn abs;
 
-    // Rows past the segment read as zero; columns past K read neighbouring bytes (their
-    // outputs are never stored).
-    __device__ __forceinline__ void load(const WeightRsrc &r, int64_t n0, int64_t p0, int64_t K) {
-        const int64_t e0 = (n0 + threadIdx.x / KQ) * K + p0 + (threadIdx.x % KQ) * 32;
-        raw = bload16(r.packed, static_cast<int>(e0 >> 1));
-        abs = absmax_bload(r, e0 >> r.bs_shift);
+    // Step n0 (segment-local row of the step's first n): rows past the segment read as zero;
+    // columns past K read neighbouring bytes (their outputs are never stored).
+    __device__ __forceinline__ void load(const WeightRsrc &r, const WAddr &ad, int64_t n0, int64_t K) {
+        raw = bload16(r.packed, ad.packed + static_cast<int>(n0 * (K >> 1)));
+        abs = absmax_bload(r, ad.block + static_cast<int>(n0 * (K >> r.bs_shift)));
     }
 
     __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, int part) const {
@@ -578,19 +584,23 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     // Two register stages (steps st+1 and st+2 in flight) and two LDS stages (st and st+1).
     // Step st computes from LDS stage (st - s0) & 1 while the other LDS stage receives step
     // st+1 from register stage (st + 1 - s0) & 1, a quarter per MFMA k-substep; the register
-    // stage of st has been consumed, so it takes the global loads of st+2.
+    // stage of st has been consumed, so it takes the global loads of st+2.  The loop body has
+    // no branches: prefetches past the range are issued anyway (in bounds of the operands or
+    // zero from the buffer range check, never consumed), so the compiler's wait counts only
+    // wait for the loads a store needs, never for the prefetch just issued.  An odd last step
+    // runs after the loop.
     FwdWeight<DT, BP> wt[2] = {};
     ActTile<BM, NT> at[2] = {};
     __syncthreads();  // tables
     const WeightRsrc wr = weight_rsrc(w);
     const rsrc_t ar = act_rsrc<BM>(a, m0);
+    const ActAddr aa = act_addr<NT>(a.ld_act);
+    const WAddr wa = fwd_waddr<BP>(wr, p0, K);
     if (s0 < s1) {
-        at[0].load(ar, a.ld_act, s0 * BR);
-        wt[0].load(wr, p0, K, s0);
-        if (s0 + 1 < s1) {
-            at[1].load(ar, a.ld_act, (s0 + 1) * BR);
-            wt[1].load(wr, p0, K, s0 + 1);
-        }
+        at[0].load(ar, aa, static_cast<int>(s0) * (BR * 2));
+        wt[0].load(wr, wa, s0);
+        at[1].load(ar, aa, static_cast<int>(s0 + 1) * (BR * 2));
+        wt[1].load(wr, wa, s0 + 1);
         at[0].store(sA[0]);
         {
             const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, s_code2));
@@ -598,30 +608,22 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
             for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
         }
         __syncthreads();
-        for (int64_t st0 = s0; st0 < s1; st0 += 2) {
+        int64_t st = s0;
+        for (; st + 1 < s1; st += 2) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int64_t st = st0 + b;
-                if (st < s1) {
-                    // On the last step the stores below write a stale stage into the LDS stage
-                    // nobody reads again: unconditional, so they interleave with the MFMAs.
-                    // stage b was drained into LDS during the previous step: refill it first,
-                    // so its loads have a whole step before they are needed
-                    if (st + 2 < s1) {
-                        at[b].load(ar, a.ld_act, (st + 2) * BR);
-                        wt[b].load(wr, p0, K, st + 2);
-                    }
-                    const Nf4Table tb =
-                        make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, s_code2));
-                    mma_step_interleaved<DT, TP, TM>(
-                        acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
-                            at[b ^ 1].store_part(sA[b ^ 1], ks);
-                            wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
-                        });
-                    __syncthreads();
-                }
+                at[b].load(ar, aa, static_cast<int>(st + b + 2) * (BR * 2));
+                wt[b].load(wr, wa, st + b + 2);
+                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, s_code2));
+                mma_step_interleaved<DT, TP, TM>(
+                    acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
+                        at[b ^ 1].store_part(sA[b ^ 1], ks);
+                        wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                    });
+                __syncthreads();
             }
         }
+        if (st < s1) mma_step<DT, TP, TM>(acc, sW[0], sA[0], wp * (BP / WP), wm * (BM / WM));
     }
     epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), w.rows, a.seg_off[seg],
                          m0 + wm * (BM / WM), split);
@@ -693,45 +695,49 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     DxWeight<DT, BP> wt[2] = {};
     ActTile<BM, NT> at[2] = {};
     const rsrc_t ar = act_rsrc<BM>(a, m0);
+    const ActAddr aa = act_addr<NT>(a.ld_act);
     __syncthreads();  // tables
     // The reduction range [s0, s1) walks the stacked segments in order; each segment runs the
     // forward kernel's pipeline (two register stages, two LDS stages, next tile's staging
-    // interleaved with the MFMAs) with its descriptor held in registers.
+    // interleaved with the MFMAs, no branches in the loop body, odd step after the loop) with
+    // its descriptor held in registers.  A segment's partial last step (rows % 64 != 0) runs
+    // unpipelined after it, with the dY columns past the segment zeroed.
     for (int seg = seg_of_step(a, s0); seg < a.nseg && a.step_start[seg] < s1; ++seg) {
-        const int64_t b0 = a.step_start[seg] > s0 ? a.step_start[seg] : s0;
+        const int64_t first = a.step_start[seg];
+        const int64_t b0 = first > s0 ? first : s0;
         const int64_t e0 = a.step_start[seg + 1] < s1 ? a.step_start[seg + 1] : s1;
         if (b0 >= e0) continue;
         const DevWeight w = a.w[seg];
         const WeightRsrc wr = weight_rsrc(w);
+        const WAddr wa = dx_waddr<BP>(wr, p0, K);
         const int64_t col_base = a.seg_off[seg];
-        const int64_t col_end = col_base + w.rows;
-        const int64_t first = a.step_start[seg];
         const float *code2 = s_code2[seg];
         float code_r[16];
         load_code_sgpr(w.code, code_r);
-        // Stage step st into register stage x; a segment's partial last step (rows % 64 != 0)
-        // has its columns past the segment zeroed (uniform branch, at most once per segment).
+        // the step holding the segment's last rows is partial unless rows % 64 == 0
+        const bool partial_last = (w.rows % BR) != 0 && e0 == a.step_start[seg + 1];
+        const int64_t e_full = partial_last ? e0 - 1 : e0;
         auto stage = [&](ActTile<BM, NT> &t, DxWeight<DT, BP> &u, int64_t st) {
-            const int64_t col0 = col_base + (st - first) * BR;
-            t.load(ar, a.ld_act, col0);
-            if (col0 + BR > col_end) t.mask(col0, col_end);
-            u.load(wr, (st - first) * BR, p0, K);
+            const int64_t n0 = (st - first) * BR;
+            t.load(ar, aa, static_cast<int>((col_base + n0) * 2));
+            u.load(wr, wa, n0, K);
         };
-        stage(at[0], wt[0], b0);
-        if (b0 + 1 < e0) stage(at[1], wt[1], b0 + 1);
-        at[0].store(sA[0]);
-        {
-            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
+        __syncthreads();  // the previous segment's last MFMAs have read the LDS stages
+        if (b0 < e_full) {
+            stage(at[0], wt[0], b0);
+            stage(at[1], wt[1], b0 + 1);
+            at[0].store(sA[0]);
+            {
+                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
 #pragma unroll
-            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
-        }
-        __syncthreads();
-        for (int64_t st0 = b0; st0 < e0; st0 += 2) {
+                for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
+            }
+            __syncthreads();
+            int64_t st = b0;
+            for (; st + 1 < e_full; st += 2) {
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const int64_t st = st0 + b;
-                if (st < e0) {
-                    if (st + 2 < e0) stage(at[b], wt[b], st + 2);
+                for (int b = 0; b < 2; ++b) {
+                    stage(at[b], wt[b], st + b + 2);
                     const Nf4Table tb =
                         make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
                     mma_step_dx<DT, BP, TP, TM>(
@@ -742,6 +748,25 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
                     __syncthreads();
                 }
             }
+            if (st < e_full) {
+                mma_step_dx<DT, BP, TP, TM>(acc, sW[0], sA[0], wp * (BP / WP), wm * (BM / WM),
+                                            [](int) {});
+                __syncthreads();
+            }
+        }
+        if (partial_last && e_full >= b0) {
+            const int64_t st = e0 - 1;
+            stage(at[0], wt[0], st);
+            at[0].mask(static_cast<int>(w.rows - (st - first) * BR));
+            at[0].store(sA[0]);
+            {
+                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
+            }
+            __syncthreads();
+            mma_step_dx<DT, BP, TP, TM>(acc, sW[0], sA[0], wp * (BP / WP), wm * (BM / WM),
+                                        [](int) {});
         }
     }
     epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), K, 0, m0 + wm * (BM / WM), split);
@@ -810,30 +835,41 @@ int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const n
     return NF4_OK;
 }
 
-// Tile choice.  The 256x256 tile (8 waves) keeps VALU dequant work under the MFMA time (it is
-// spread over 256 rows of activations); the 128x128 tile (4 waves, 2 workgroups per CU) is VALU-
-// bound and only used when the big tiles cannot fill half of the GPU even with split-K.  The
-// reduction is split into at most kCUs / tiles parts of at least kMinSteps steps each.
-constexpr int kMinSteps = 6;
+// Tile and split choice by a cost model whose constants were measured on MI355X (fp16, M = 2048,
+// every Qwen2.5-1.5B projection, each plan timed): one 64-deep step of a 256x256 tile takes
+// ~2.6 us with one workgroup per CU; a 128x128 step ~1.35 us alone on a CU and ~1.6 us with two
+// workgroups per CU.  Workgroups run in rounds of 256 (256x256) or 512 (128x128).  Split-K adds
+// the fp32 partial round trip (written by the GEMM, read back by the reduction) at ~5 TB/s plus
+// ~12 us of reduction launch and tail.  The larger tile needs 4x fewer dequant instructions per
+// MFMA, which the step times already contain.
+constexpr int kMaxSplits = 16;
 
-int splits_for(int64_t tiles, int64_t steps, int per_cu) {
-    int64_t s = (kCUs * per_cu) / (tiles > 0 ? tiles : 1);
-    const int64_t by_steps = steps / kMinSteps;
-    if (s > by_steps) s = by_steps;
-    if (s > 16) s = 16;
-    return s < 1 ? 1 : static_cast<int>(s);
+double plan_cost(int cfg, int64_t tiles, int splits, int64_t steps, int64_t out_elems) {
+    const int64_t blocks = tiles * splits;
+    const int64_t slots = cfg == 0 ? kCUs : 2 * kCUs;
+    const int64_t per = (steps + splits - 1) / splits;
+    const double t_step = cfg == 0 ? 2.6 : (blocks <= kCUs ? 1.35 : 1.6);
+    double c = double((blocks + slots - 1) / slots) * double(per) * t_step + 1.0;
+    if (splits > 1) c += 2.0 * double(splits) * double(out_elems) * 4.0 / 5.0e6 + 12.0;
+    return c;
 }
 
-Plan make_plan(int64_t big, int64_t small, int64_t steps) {
-    Plan p{};
-    const int sb = big >= kCUs ? 1 : splits_for(big, steps, 1);
-    if (big * sb >= kCUs / 2) {
-        p.cfg = 0; p.bp = 256; p.bm = 256; p.tiles = big; p.splits = sb;
-    } else {
-        p.cfg = 1; p.bp = 128; p.bm = 128; p.tiles = small;
-        p.splits = small >= 2 * kCUs ? 1 : splits_for(small, steps, 2);
+Plan make_plan(int64_t big, int64_t small, int64_t steps, int64_t out_elems) {
+    Plan best{};
+    double best_cost = 0.0;
+    for (int cfg = 0; cfg < 2; ++cfg) {
+        const int64_t tiles = cfg == 0 ? big : small;
+        for (int s = 1; s <= kMaxSplits; ++s) {
+            const int64_t per = (steps + s - 1) / s;
+            if (s > 1 && (s - 1) * per >= steps) break;  // no empty split
+            const double c = plan_cost(cfg, tiles, s, steps, out_elems);
+            if (best.splits == 0 || c < best_cost) {
+                best = Plan{cfg, cfg == 0 ? 256 : 128, cfg == 0 ? 256 : 128, s, tiles};
+                best_cost = c;
+            }
+        }
     }
-    return p;
+    return best;
 }
 
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
@@ -844,7 +880,9 @@ Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
     }
     big *= (m + 255) / 256;
     small *= (m + 127) / 128;
-    return make_plan(big, small, ws[0].cols / BR);
+    int64_t n = 0;
+    for (int i = 0; i < nw; ++i) n += ws[i].rows;
+    return make_plan(big, small, ws[0].cols / BR, m * n);
 }
 
 Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
@@ -853,7 +891,7 @@ Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
     const int64_t K = ws[0].cols;
     const int64_t big = ((K + 255) / 256) * ((m + 255) / 256);
     const int64_t small = ((K + 127) / 128) * ((m + 127) / 128);
-    return make_plan(big, small, steps);
+    return make_plan(big, small, steps, m * K);
 }
 
 template <int DT>
