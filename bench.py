@@ -10,9 +10,13 @@ quant, LoRA A kaiming-uniform, B N(0,0.01), dY N(0,1e-3)) and resident in HBM be
 Prints ONE JSON line: value = algorithmic TFLOP/s of the whole step (384.28 GFLOP), the
 roofline of the dominant GEMM kernel (HIP events around its launches, on the launch stream),
 the standalone dequant's HBM GB/s over the 28-layer stack (3.3 GB), and the CPU oracle timed on
-the host cores as a baseline.
+the host cores as a baseline.  The other BASELINE configs ride along in the same line:
+`varlen_stack` (config 3: the 28-layer Qwen2.5-1.5B projection stack on a varlen batch),
+`qwen7b_m8192` (config 4: a Qwen2.5-7B layer in bf16 at M=8192) and `gemv_15b` / `gemv_7b`
+(config 4: forward over the 28-layer stacks at M in {1, 8, 64}, HBM GB/s).
 
     python bench.py [--steps K] [--warmup W] [--dtype f16|bf16] [--no-cpu-baseline]
+                    [--no-dequant] [--no-stack] [--no-7b] [--no-gemv]
 """
 
 from __future__ import annotations
@@ -53,6 +57,12 @@ def parse():
     ap.add_argument("--dtype", choices=["f16", "bf16"], default="f16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dequant", action="store_true")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip the 28-layer varlen projection stack (config 3)")
+    ap.add_argument("--no-7b", action="store_true",
+                    help="skip the Qwen2.5-7B bf16 M=8192 layer (config 4)")
+    ap.add_argument("--no-gemv", action="store_true",
+                    help="skip the small-M forward sweeps over the 28-layer stacks")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times: the "
@@ -63,79 +73,15 @@ def parse():
 # ----------------------------------------------------------------------------- workload
 
 class Workload:
-    """Weights, inputs and every output buffer of one step, plus prebuilt C-ABI arguments."""
+    """One Qwen2.5-1.5B layer on the projection-stack driver: weights,
+    inputs, every output buffer and the prebuilt C-ABI arguments of one step."""
 
     def __init__(self, dtype, dev):
-        import torch
+        from solution.stack import QWEN2_15B, ProjectionStack
 
-        from solution import _lib
-        from solution.quant_state import quantize_4bit, weight_desc
-
-        self.torch, self.dev, self.dtype = torch, dev, dtype
-        self.lib = _lib.load()
-        self.dt = _lib.DTYPE_CODE[dtype]
-        self.W = {}
-        for i, (name, n, k) in enumerate(LAYER):
-            g = torch.Generator(device=dev).manual_seed(100 + i)
-            w = torch.randn(n, k, generator=g, device=dev) * 0.02
-            packed, qs = quantize_4bit(w)
-            self.W[name] = (packed.view(-1), qs)
-        del w
-
-        def rnd(shape, seed, std=1.0):
-            g = torch.Generator(device=dev).manual_seed(seed)
-            return (torch.randn(shape, generator=g, device=dev) * std).to(dtype)
-
-        H, I, QKV = 1536, 8960, 2048
-        self.x = rnd((M, H), 1)            # input of q|k|v (and LoRA)
-        self.attn = rnd((M, H), 11)        # input of o
-        self.x2 = rnd((M, H), 12)          # input of gate|up
-        self.act = rnd((M, I), 13)         # input of down
-        self.bias_qkv = rnd((QKV,), 14, 0.1)
-        g = torch.Generator(device=dev).manual_seed(3)
-        bound = 1.0 / H ** 0.5
-        self.a_q = ((torch.rand(RANK, H, generator=g, device=dev) * 2 - 1) * bound).to(dtype)
-        self.a_v = ((torch.rand(RANK, H, generator=g, device=dev) * 2 - 1) * bound).to(dtype)
-        g = torch.Generator(device=dev).manual_seed(4)
-        self.b_q = (torch.randn(1536, RANK, generator=g, device=dev) * 0.01).to(dtype)
-        self.b_v = (torch.randn(256, RANK, generator=g, device=dev) * 0.01).to(dtype)
-        self.scale = ALPHA / RANK
-        self.dy_qkv = rnd((M, QKV), 2, 1e-3)
-        self.dy_o = rnd((M, H), 21, 1e-3)
-        self.dy_gu = rnd((M, 2 * I), 22, 1e-3)
-        self.dy_d = rnd((M, H), 23, 1e-3)
-
-        e = lambda *s: torch.empty(s, dtype=dtype, device=dev)  # noqa: E731
-        self.t_q, self.t_v = e(M, RANK), e(M, RANK)
-        self.y_qkv, self.y_o, self.y_gu, self.y_d = e(M, QKV), e(M, H), e(M, 2 * I), e(M, H)
-        self.dx_d, self.dx_gu, self.dx_o, self.dx_qkv = e(M, I), e(M, H), e(M, H), e(M, H)
-        self.da_q, self.da_v = e(M, RANK), e(M, RANK)
-        f = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)  # noqa: E731
-        self.gb_q, self.gb_v, self.ga_q, self.ga_v = f(1536, RANK), f(256, RANK), f(RANK, H), \
-            f(RANK, H)
-
-        arr = lambda names: _lib.NF4Weight * len(names)  # noqa: E731
-        self.groups = {}
-        for gname, names in (("qkv", ["q", "k", "v"]), ("o", ["o"]), ("gu", ["gate", "up"]),
-                             ("down", ["down"])):
-            descs = arr(names)(*[weight_desc(*self.W[nm]) for nm in names])
-            self.groups[gname] = descs
-        lib, dt = self.lib, self.dt
-        self.ws = {}
-        for gname, descs in self.groups.items():
-            nw = len(descs)
-            fb = lib.nf4_linear_fwd_workspace(M, descs, nw, dt)
-            db = lib.nf4_linear_dx_workspace(M, descs, nw, dt)
-            self.ws[gname] = (torch.empty(max(fb, 1), dtype=torch.uint8, device=dev), fb,
-                              torch.empty(max(db, 1), dtype=torch.uint8, device=dev), db)
-        wb = lib.nf4_lora_wgrad_workspace(M, 1536, RANK)
-        self.wg_ws = (torch.empty(wb, dtype=torch.uint8, device=dev), wb)
-        P = lambda t: t.data_ptr()  # noqa: E731
-        L = _lib.NF4Lora
-        self.fwd_loras = (L * 2)(L(0, RANK, self.scale, P(self.t_q), P(self.b_q), None, None),
-                                 L(2, RANK, self.scale, P(self.t_v), P(self.b_v), None, None))
-        self.dx_loras = (L * 2)(L(0, RANK, self.scale, None, None, P(self.a_q), P(self.da_q)),
-                                L(2, RANK, self.scale, None, None, P(self.a_v), P(self.da_v)))
+        self.stack = ProjectionStack.synthetic(QWEN2_15B, 1, M, dtype, dev, seed_base=100,
+                                               rank=RANK, alpha=ALPHA)
+        self.lib = self.stack.lib
 
     # flops of one step, counted from the shapes
     @staticmethod
@@ -163,64 +109,108 @@ class Workload:
     def step(self, ev=None):
         """Queue one forward+backward on torch's current stream.  `ev`: dict name -> (start,
         end) events recorded around each fused GEMM launch."""
-        lib, dt, s = self.lib, self.dt, self.torch.cuda.current_stream().cuda_stream
-        P = lambda t: t.data_ptr()  # noqa: E731
-        chk = self._chk
+        self.stack.step(ev)
 
-        def timed(name, fn):
-            if ev is not None:
-                ev[name][0].record()
-            chk(fn(), name)
-            if ev is not None:
-                ev[name][1].record()
 
-        H, I, QKV = 1536, 8960, 2048
-        chk(lib.nf4_lora_xa(P(self.x), M, H, H, P(self.a_q), RANK, P(self.t_q), dt, s), "xa")
-        chk(lib.nf4_lora_xa(P(self.x), M, H, H, P(self.a_v), RANK, P(self.t_v), dt, s), "xa")
-        G, W = self.groups, self.ws
-        timed("fwd_qkv", lambda: lib.nf4_linear_fwd(
-            P(self.x), M, H, G["qkv"], 3, P(self.bias_qkv), self.fwd_loras, 2, P(self.y_qkv), QKV,
-            dt, P(W["qkv"][0]), W["qkv"][1], s))
-        timed("fwd_o", lambda: lib.nf4_linear_fwd(
-            P(self.attn), M, H, G["o"], 1, None, None, 0, P(self.y_o), H, dt, P(W["o"][0]),
-            W["o"][1], s))
-        timed("fwd_gu", lambda: lib.nf4_linear_fwd(
-            P(self.x2), M, H, G["gu"], 2, None, None, 0, P(self.y_gu), 2 * I, dt, P(W["gu"][0]),
-            W["gu"][1], s))
-        timed("fwd_down", lambda: lib.nf4_linear_fwd(
-            P(self.act), M, I, G["down"], 1, None, None, 0, P(self.y_d), H, dt,
-            P(W["down"][0]), W["down"][1], s))
-        # backward
-        timed("dx_down", lambda: lib.nf4_linear_dx(
-            P(self.dy_d), M, H, G["down"], 1, None, 0, P(self.dx_d), I, 0, dt, P(W["down"][2]),
-            W["down"][3], s))
-        timed("dx_gu", lambda: lib.nf4_linear_dx(
-            P(self.dy_gu), M, 2 * I, G["gu"], 2, None, 0, P(self.dx_gu), H, 0, dt,
-            P(W["gu"][2]), W["gu"][3], s))
-        timed("dx_o", lambda: lib.nf4_linear_dx(
-            P(self.dy_o), M, H, G["o"], 1, None, 0, P(self.dx_o), H, 0, dt, P(W["o"][2]),
-            W["o"][3], s))
-        dq = self.dy_qkv
-        chk(lib.nf4_lora_da(P(dq), M, 1536, QKV, P(self.b_q), RANK, self.scale, P(self.da_q),
-                            dt, s), "da")
-        chk(lib.nf4_lora_da(P(dq) + 1792 * dq.element_size(), M, 256, QKV, P(self.b_v), RANK,
-                            self.scale, P(self.da_v), dt, s), "da")
-        wg, wb = P(self.wg_ws[0]), self.wg_ws[1]
-        chk(lib.nf4_lora_wgrad(P(dq), M, 1536, QKV, P(self.t_q), RANK, self.scale,
-                               P(self.gb_q), 0, dt, wg, wb, s), "wgrad")
-        chk(lib.nf4_lora_wgrad(P(dq) + 1792 * dq.element_size(), M, 256, QKV, P(self.t_v), RANK,
-                               self.scale, P(self.gb_v), 0, dt, wg, wb, s), "wgrad")
-        chk(lib.nf4_lora_wgrad(P(self.x), M, H, H, P(self.da_q), RANK, 1.0, P(self.ga_q), 1, dt,
-                               wg, wb, s), "wgrad")
-        chk(lib.nf4_lora_wgrad(P(self.x), M, H, H, P(self.da_v), RANK, 1.0, P(self.ga_v), 1, dt,
-                               wg, wb, s), "wgrad")
-        timed("dx_qkv", lambda: lib.nf4_linear_dx(
-            P(dq), M, QKV, G["qkv"], 3, self.dx_loras, 2, P(self.dx_qkv), H, 0, dt,
-            P(W["qkv"][2]), W["qkv"][3], s))
+def _time_steps(torch, fn, steps, warmup):
+    """Mean ms of `fn` over `steps` runs after `warmup`, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
-    def _chk(self, st, what):
-        if st != 0:
-            raise RuntimeError(f"{what}: status {st} ({self.lib.nf4_status_string(st).decode()})")
+
+# -------------------------------------------------------------------- varlen stack (config 3)
+
+def varlen_stack_leg(dtype, dev, steps=5, warmup=2, gemv=True):
+    """the 28-layer Qwen2.5-1.5B projection stack (7 NF4 weights per layer,
+    seeds 1000 + 7 l + i) forward and backward on an unpadded batch of 4 sequences with lengths
+    drawn uniformly from [64, 512] (seed 5), concatenated through cu_seqlens."""
+    import torch
+
+    from solution.stack import QWEN2_15B, ProjectionStack
+
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(64, 513, (4,), generator=g)
+    cu = torch.zeros(5, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    st = ProjectionStack.synthetic(QWEN2_15B, 28, int(cu[-1]), dtype, dev, seed_base=1000,
+                                   seed_stride=7, rank=RANK, alpha=ALPHA)
+    m = st.set_tokens(cu)
+    ms = _time_steps(torch, st.step, steps, warmup)
+    fl = st.flops()["total"]
+    tf = fl / (ms * 1e-3) / 1e12
+    out = {"varlen_stack": {
+        "workload": "28-layer Qwen2.5-1.5B projection stack fwd+bwd, varlen tokens",
+        "cu_seqlens": [int(v) for v in cu], "tokens": m, "ms_per_step": round(ms, 3),
+        "gflop_per_step": round(fl / 1e9, 2), "tflops": round(tf, 2),
+        "frac": round(tf / PEAK_MFMA_TFLOPS, 4), "steps": steps}}
+    if gemv:
+        out["gemv_15b"] = gemv_sweep(st, torch, "28-layer Qwen2.5-1.5B stack, fp16")
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
+# ------------------------------------------------------------ 7B bf16 and GEMV sweep (config 4)
+
+def qwen7b_legs(dev, steps=5, warmup=2, gemv=True, layers=28):
+    """one Qwen2.5-7B layer (hidden 3584, intermediate 18944, kv 512) in
+    bf16 at M = 8192, forward+backward; and the small-M dequant-GEMV regime (M in {1, 8, 64},
+    forward) over the 28-layer 7B stack (3.3 GB of NF4 weights, far above the Infinity Cache),
+    reported as HBM GB/s (NF4 weight bytes + activation bytes) against 8 TB/s."""
+    import torch
+
+    from solution.stack import GEMMS, QWEN2_7B, ProjectionStack
+
+    st = ProjectionStack.synthetic(QWEN2_7B, layers if gemv else 1, 8192, torch.bfloat16, dev,
+                                   seed_base=2000, seed_stride=7, rank=RANK, alpha=ALPHA)
+    st.set_tokens([0, 8192])
+    ev = {n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for n in GEMMS}
+    fl = st.flops()["total"] / len(st.per_layer)
+    ms = _time_steps(torch, lambda: (st.forward(layers=[0]), st.backward(layers=[0])), steps,
+                     warmup)
+    st.forward(ev, layers=[0])
+    st.backward(ev, layers=[0])
+    torch.cuda.synchronize()
+    per = {n: round(ev[n][0].elapsed_time(ev[n][1]) * 1e3, 1) for n in GEMMS}
+    tf = fl / (ms * 1e-3) / 1e12
+    out = {"qwen7b_m8192": {
+        "workload": "Qwen2.5-7B decoder-layer NF4 projections fwd+bwd, bf16, M=8192",
+        "ms_per_step": round(ms, 3), "gflop_per_step": round(fl / 1e9, 1),
+        "tflops": round(tf, 2), "frac": round(tf / PEAK_MFMA_TFLOPS, 4),
+        "gemm_us_per_launch": per}}
+    if gemv:
+        out["gemv_7b"] = gemv_sweep(st, torch, "28-layer Qwen2.5-7B stack, bf16")
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
+def gemv_sweep(st, torch, what, ms_list=(1, 8, 64), reps=5):
+    """Forward of every layer of `st` at M tokens: GB/s = (NF4 weight bytes + activations read
+    and written) / time."""
+    res = {"workload": f"forward of the {what} at M in {list(ms_list)} (decode regime)"}
+    wbytes = st.weight_bytes()
+    sh, es = st.shape, st.x.element_size()
+    for m in ms_list:
+        st.set_tokens([0, m])
+        act = len(st.per_layer) * m * es * (
+            (sh.hidden + st.n_qkv) + 2 * sh.hidden + (sh.hidden + 2 * sh.inter) +
+            (sh.inter + sh.hidden) + 2 * 2 * st.rank)
+        ms = _time_steps(torch, st.forward, reps, 1)
+        gbps = (wbytes + act) / (ms * 1e-3) / 1e9
+        res[str(m)] = {"us_per_layer": round(ms * 1e3 / len(st.per_layer), 2),
+                       "gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4)}
+    res["nf4_weight_bytes"] = wbytes
+    return res
 
 
 # ------------------------------------------------------------------------------ dequant leg
@@ -442,6 +432,10 @@ def main():
         out["dequant"] = dict(dq, roofline={"bound": "hbm", "achieved": dq["gbps"],
                                             "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                             "frac": dq["frac"], "traffic": None})
+    if not args.no_stack:
+        out.update(varlen_stack_leg(dtype, dev, gemv=not args.no_gemv))
+    if not args.no_7b:
+        out.update(qwen7b_legs(dev, gemv=not args.no_gemv))
     if args.copy_mib > 0:
         src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)

@@ -116,3 +116,13 @@ def test_layers_to_dequant_signature():
 
     with pytest.raises(ValueError):
         _dequant([], torch.float16, streamed=[(None, None)])
+
+
+def test_cu_seqlens_validation():
+    from solution.stack import tokens_from_cu_seqlens
+
+    assert tokens_from_cu_seqlens([0, 64, 200, 201]) == 201
+    assert tokens_from_cu_seqlens(torch.tensor([0], dtype=torch.int32)) == 0
+    for bad in ([1, 5], [0, 5, 3], [[0, 1]]):
+        with pytest.raises(ValueError):
+            tokens_from_cu_seqlens(bad)
