@@ -112,6 +112,27 @@ class Workload:
         self.stack.step(ev)
 
 
+def _time_graph(torch, fn, reps, warmup=1):
+    """Mean ms of one replay of a HIP graph captured from `fn` (its launches queued on the
+    capture stream): launch-bound sequences measured without per-launch host overhead."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / reps
+
+
 def _time_steps(torch, fn, steps, warmup):
     """Mean ms of `fn` over `steps` runs after `warmup`, HIP events on the current stream."""
     for _ in range(warmup):
@@ -195,9 +216,11 @@ def qwen7b_legs(dev, steps=5, warmup=2, gemv=True, layers=28):
 
 
 def gemv_sweep(st, torch, what, ms_list=(1, 8, 64), reps=5):
-    """Forward of every layer of `st` at M tokens: GB/s = (NF4 weight bytes + activations read
-    and written) / time."""
-    res = {"workload": f"forward of the {what} at M in {list(ms_list)} (decode regime)"}
+    """Forward of every layer of `st` at M tokens, captured once in a HIP graph and replayed
+    (decode runs launch-bound otherwise): GB/s = (NF4 weight bytes + activations read and
+    written) / replay time."""
+    res = {"workload": f"forward of the {what} at M in {list(ms_list)} (decode regime), "
+                       f"HIP graph replay"}
     wbytes = st.weight_bytes()
     sh, es = st.shape, st.x.element_size()
     for m in ms_list:
@@ -205,10 +228,12 @@ def gemv_sweep(st, torch, what, ms_list=(1, 8, 64), reps=5):
         act = len(st.per_layer) * m * es * (
             (sh.hidden + st.n_qkv) + 2 * sh.hidden + (sh.hidden + 2 * sh.inter) +
             (sh.inter + sh.hidden) + 2 * 2 * st.rank)
-        ms = _time_steps(torch, st.forward, reps, 1)
+        ms = _time_graph(torch, st.forward, reps)
+        eager = _time_steps(torch, st.forward, reps, 1)
         gbps = (wbytes + act) / (ms * 1e-3) / 1e9
         res[str(m)] = {"us_per_layer": round(ms * 1e3 / len(st.per_layer), 2),
-                       "gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4)}
+                       "gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                       "us_per_layer_eager_launches": round(eager * 1e3 / len(st.per_layer), 2)}
     res["nf4_weight_bytes"] = wbytes
     return res
 
@@ -232,9 +257,10 @@ def dequant_leg(dtype, dev, reps=5):
         packed, qs = quantize_4bit(torch.randn(n, k, generator=g, device=dev) * 0.02)
         base[name] = (packed.view(-1), qs)
     groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
-    launches, keep = [], []
+    grouped, batched, keep = [], [], []
     total_bytes = 0
     for layer in range(28):
+        layer_descs, layer_outs = [], []
         for names in groups:
             descs, rows = [], 0
             for nm in names:
@@ -247,29 +273,40 @@ def dequant_leg(dtype, dev, reps=5):
             out = torch.empty((rows, cols), dtype=dtype, device=dev)
             keep.append(out)
             arr = (_lib.NF4Weight * len(descs))(*descs)
-            launches.append((arr, len(descs), out.data_ptr()))
+            grouped.append((arr, len(descs), out.data_ptr()))
             total_bytes += dequant_bytes(rows * cols)
-    s = torch.cuda.current_stream().cuda_stream
+            off = 0
+            for d, nm in zip(descs, names):  # the same outputs, weight by weight
+                layer_descs.append(d)
+                layer_outs.append(out.data_ptr() + off * out.element_size())
+                off += int(base[nm][1].shape[0]) * cols
+        batched.append(((_lib.NF4Weight * 7)(*layer_descs),
+                        (ctypes.c_void_p * 7)(*layer_outs)))
 
-    def run():
-        for arr, nw, out in launches:
+    def run_grouped():
+        s = torch.cuda.current_stream().cuda_stream
+        for arr, nw, out in grouped:
             st = lib.nf4_dequant_multi(arr, nw, out, dt, s)
             if st:
                 raise RuntimeError(f"nf4_dequant_multi status {st}")
 
-    run()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    sec = e0.elapsed_time(e1) / 1e3 / reps
-    gbps = total_bytes / sec / 1e9
+    def run_batched():
+        s = torch.cuda.current_stream().cuda_stream
+        for arr, outs in batched:
+            st = lib.nf4_dequant_batch(arr, 7, outs, dt, s)
+            if st:
+                raise RuntimeError(f"nf4_dequant_batch status {st}")
+
+    batch_ms = _time_graph(torch, run_batched, reps)
+    group_ms = _time_graph(torch, run_grouped, reps)
+    gbps = total_bytes / (batch_ms * 1e-3) / 1e9
     return {"gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
-            "bytes_per_pass": total_bytes, "us_per_pass": round(sec * 1e6, 1),
-            "launches_per_pass": len(launches), "working_set": "28-layer Qwen2.5-1.5B stack"}
+            "bytes_per_pass": total_bytes, "us_per_pass": round(batch_ms * 1e3, 1),
+            "launches_per_pass": len(batched), "working_set": "28-layer Qwen2.5-1.5B stack",
+            "timing": "one nf4_dequant_batch launch per layer (7 weights), HIP graph replay",
+            "gbps_grouped_launches": round(total_bytes / (group_ms * 1e-3) / 1e9, 1),
+            "grouped": "4 nf4_dequant_multi launches per layer (q|k|v, o, gate|up, down) as the "
+                       "reference's _dequant groups them"}
 
 
 # ---------------------------------------------------------------------------- CPU baseline

@@ -90,6 +90,13 @@ int nf4_dequant(const nf4_weight *w, void *out, int out_dtype, void *stream);
 #define NF4_MAX_SEGMENTS 8
 int nf4_dequant_multi(const nf4_weight *ws, int nw, void *out, int out_dtype, void *stream);
 
+/* Up to NF4_MAX_SEGMENTS weights of any shapes in one launch, weight i into its own
+ * [rows_i, cols_i] buffer outs[i] (e.g. all seven projections of a decoder layer).
+ * Replaces: the reference's per-layer sequence of _dequant / dequantize_nf4 calls, one kernel
+ *           launch per call (/root/reference/solution/layer.py:463-493; nf4.py:69-77). */
+int nf4_dequant_batch(const nf4_weight *ws, int nw, void *const *outs, int out_dtype,
+                      void *stream);
+
 /* ------------------------------------------------------------------ fused dequant-GEMMs */
 
 /* Y[M, sum(rows)] = X[M, K] @ W_stack^T (+ bias) (+ sum over loras scale * T @ B^T on the

@@ -160,6 +160,33 @@ __device__ __forceinline__ void load_code_sgpr(const float *code, float (&out)[1
         out[i] = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, code[i])));
 }
 
+// ----------------------------------------------------------------- buffer resources
+//
+// Main-loop loads go through buffer resources: an offset at or past the resource's byte range
+// returns zero in hardware.  Every lane then issues the same unconditional loads (no divergent
+// branches in the pipeline, so the compiler's wait counters stay exact), rows past M and weight
+// rows past the segment read as zero, and nothing outside an operand is ever touched.
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+    const int n = bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : static_cast<int>(bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), n,
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4_t bload16(rsrc_t r, int off) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload2(rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload1(rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
 static inline int status_of(hipError_t e) { return e == hipSuccess ? NF4_OK : NF4_ERR_LAUNCH; }
 
 static inline bool aligned(const void *p, uintptr_t a) {

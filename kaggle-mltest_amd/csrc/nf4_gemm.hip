@@ -72,7 +72,8 @@ struct GemmArgs {
     int64_t ld_out;
     int64_t n_out;                // forward: sum rows; dx: K
     float *partial;               // split workspace [splits][M][n_out] or null
-    int splits;
+    int splits;                   // reduction splits = gridDim.y
+    int64_t per_split;            // reduction steps per split (host-computed: no divisions)
     int64_t m_tiles;
     int64_t p_tiles;              // dx: tiles along K
     int64_t total_steps;          // dx: sum of step counts
@@ -129,33 +130,6 @@ __device__ __forceinline__ float absmax_val(const DevWeight &w, const AbsIn &in,
     return w.nested ? __fadd_rn(__fmul_rn(code2[in.q], in.s), w.offset) : in.s;
 }
 
-// ----------------------------------------------------------------- buffer resources
-//
-// Main-loop loads go through buffer resources: an offset at or past the resource's byte range
-// returns zero in hardware.  Every lane then issues the same unconditional loads (no divergent
-// branches in the pipeline, so the compiler's wait counters stay exact), rows past M and weight
-// rows past the segment read as zero, and nothing outside an operand is ever touched.
-
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
-    const int n = bytes > 0x7fffffff ? 0x7fffffff : (bytes < 0 ? 0 : static_cast<int>(bytes));
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), n,
-                                             0x00020000);
-}
-__device__ __forceinline__ u32x4_t bload16(rsrc_t r, int off) {
-    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-__device__ __forceinline__ uint32_t bload4(rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t bload2(rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t bload1(rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
-}
-
 // Resources of one weight: packed bytes, uint8 absmax codes (nested) and the fp32 scale array
 // (absmax2 when nested, the fp32 absmax otherwise).
 struct WeightRsrc {
@@ -164,9 +138,10 @@ struct WeightRsrc {
     int bs_shift, bs2_shift;
 };
 
+// (The fused kernels take power-of-two block sizes only: shifts, no 64-bit divisions.)
 __device__ __forceinline__ WeightRsrc weight_rsrc(const DevWeight &w) {
     const int64_t n = w.rows * w.cols;
-    const int64_t nb = (n + w.blocksize - 1) / w.blocksize;
+    const int64_t nb = (n + w.blocksize - 1) >> w.bs_shift;
     WeightRsrc r;
     r.packed = make_rsrc(w.packed, (n + 1) / 2);
     r.nested = w.nested;
@@ -174,7 +149,7 @@ __device__ __forceinline__ WeightRsrc weight_rsrc(const DevWeight &w) {
     r.bs2_shift = w.bs2_shift;
     if (w.nested) {
         r.q = make_rsrc(w.absmax, nb);
-        r.s = make_rsrc(w.absmax2, ((nb + w.blocksize2 - 1) / w.blocksize2) * 4);
+        r.s = make_rsrc(w.absmax2, ((nb + w.blocksize2 - 1) >> w.bs2_shift) * 4);
     } else {
         r.q = make_rsrc(w.absmax, 0);
         r.s = make_rsrc(w.absmax, nb * 4);
@@ -522,17 +497,19 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
     __shared__ float s_code2[256];
 
-    const int64_t bid = blockIdx.x;
-    const int split = static_cast<int>(bid % a.splits);
-    const int64_t tile = bid / a.splits;
+    // grid: x = tile (segments in order, m fastest), y = reduction split.  32-bit tile
+    // arithmetic: 64-bit divisions are long scalar sequences the whole CU waits on.
+    const int split = blockIdx.y;
+    const int64_t tile = blockIdx.x;
     const int seg = seg_of_tile(a, tile);
-    const int64_t local = tile - a.tile_start[seg];
-    const int64_t p0 = (local / a.m_tiles) * BP;
-    const int64_t m0 = (local % a.m_tiles) * BM;
+    const uint32_t local = static_cast<uint32_t>(tile - a.tile_start[seg]);
+    const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
+    const int64_t p0 = static_cast<int64_t>(local / mtl) * BP;
+    const int64_t m0 = static_cast<int64_t>(local % mtl) * BM;
     const DevWeight w = a.w[seg];  // by value: kept in registers for the whole loop
     const int64_t K = a.K;
     const int64_t steps = K / BR;
-    const int64_t per = (steps + a.splits - 1) / a.splits;
+    const int64_t per = a.per_split;
     const int64_t s0 = split * per;
     const int64_t s1 = s0 + per < steps ? s0 + per : steps;
 
@@ -629,6 +606,165 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
                          m0 + wm * (BM / WM), split);
 }
 
+// ------------------------------------------------------------------- small-M forward path
+//
+// Y = X W^T for M <= 32 * MT tokens, MT 1 or 2 (the decode regime), bound by reading the packed
+// weights.  A workgroup owns 32 weight rows of one segment; its NW waves split the reduction,
+// each dequantizing its rows straight into MFMA A-fragment registers (no LDS staging) and
+// reading its activation B-fragments from global memory (rows >= M read as zero from the
+// buffer range check).  Inside a 64-deep step both operands use the same k order: lane half h
+// takes k = 32h .. 32h+31 and k-substep ks the 8 values 32h + 8ks .. 32h + 8ks + 7, so each lane
+// loads its row's 16 packed bytes and its activation row's 64 bytes contiguously.  The NW
+// partial tiles are added through LDS in wave order (deterministic) and leave through the GEMM
+// epilogue.  At most 128 VGPRs for one activation fragment (four waves per SIMD keep enough
+// loads in flight), 256 for two.
+template <int DT, int MT, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 ? 4 : 2)))
+void gemv_kernel(const GemmArgs a) {
+    __shared__ float s_code2[256];
+    __shared__ float4_t s_red[NW / 2][MT * 4][64];
+
+    const int split = blockIdx.y;
+    const int64_t tile = blockIdx.x;
+    const int seg = seg_of_tile(a, tile);
+    const int64_t p0 = (tile - a.tile_start[seg]) * 32;
+    const DevWeight w = a.w[seg];
+    const int64_t K = a.K;
+    const int64_t steps = K / BR;
+    const int64_t per = a.per_split;
+    const int64_t s0 = split * per;
+    const int64_t s1 = s0 + per < steps ? s0 + per : steps;
+    // wave-uniform: the step range below lives in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int64_t pw = (s1 - s0 + NW - 1) / NW;
+    const int64_t w0 = s0 + wave * pw;
+    const int64_t w1 = w0 + pw < s1 ? w0 + pw : s1;
+
+    const WeightRsrc wr = weight_rsrc(w);
+    const int r = lane & 31, h = lane >> 5;
+    const int64_t row = p0 + r;
+    const int wpk = static_cast<int>(row * (K >> 1) + 16 * h);
+    const int wblk = static_cast<int>(row * (K >> wr.bs_shift));
+    const int64_t mrows = a.M < 32 * MT ? a.M : 32 * MT;
+    const rsrc_t xr = make_rsrc(a.act, ((mrows - 1) * a.ld_act + a.act_cols) * 2);
+    int xoff[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) xoff[j] = static_cast<int>(((j * 32 + r) * a.ld_act + 32 * h) * 2);
+
+    // Three register stages of (weights, activations), loaded three steps ahead and issued
+    // before anything else, so their latency overlaps the table loads.  Prefetch steps are
+    // clamped to the wave's last step, so they re-read cached bytes instead of fetching other
+    // waves' rows; the loop body has no branches.
+    struct Stage {
+        u32x4_t raw;
+        AbsIn abs;
+        u32x4_t x[MT][4];
+    };
+    auto load = [&](Stage &g, int64_t st) {
+        g.raw = bload16(wr.packed, wpk + static_cast<int>(st) * (BR / 2));
+        g.abs = absmax_bload(wr, wblk + static_cast<int>((st * BR) >> wr.bs_shift));
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                g.x[j][ks] = bload16(xr, xoff[j] + static_cast<int>(st) * (BR * 2) + ks * 16);
+    };
+    // table loads first: waiting for them (in issue order) then never waits for the prefetch
+    float c2 = 0.f;
+    if (w.nested && threadIdx.x < 256) c2 = w.code2[threadIdx.x];
+    float code_r[16];
+    load_code_sgpr(w.code, code_r);
+    const int64_t last = w1 > w0 ? w1 - 1 : w0;
+    auto cl = [&](int64_t v) { return v < last ? v : last; };
+    Stage g[3];
+#pragma unroll
+    for (int b = 0; b < 3; ++b) load(g[b], cl(w0 + b));
+    if (w.nested && threadIdx.x < 256) s_code2[threadIdx.x] = c2;
+
+    float16_t acc[1][MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[0][j] = (float16_t){};
+    __syncthreads();  // tables
+
+    // LoRA slab on the last wave (the one with the fewest steps) of split 0:
+    // acc = scale * B[p rows] . T[m rows]^T, before its share of the weight product
+    const LoraDev &lo = a.lora[seg];
+    if (lo.has && split == 0 && wave == NW - 1) {
+        const int kh = h * 8;
+        for (int k0 = 0; k0 < lo.rank; k0 += 16) {
+            const int lim = lo.rank - (k0 + kh);
+            const u32x4_t fa = (row < w.rows && lim > 0) ? gather8(lo.b + row * lo.rank + k0 + kh, 1, lim)
+                                                         : (u32x4_t){0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+                const int64_t m = j * 32 + r;
+                const u32x4_t fb = (m < a.M && lim > 0) ? gather8(lo.t + m * lo.rank + k0 + kh, 1, lim)
+                                                        : (u32x4_t){0u, 0u, 0u, 0u};
+                acc[0][j] = mfma32<DT>(fa, fb, acc[0][j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MT; ++j) acc[0][j] *= lo.scale;
+    }
+
+    auto compute = [&](const Stage &g) {
+        const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, g.abs, s_code2));
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint32_t wd = ks == 0 ? g.raw.x : ks == 1 ? g.raw.y : ks == 2 ? g.raw.z : g.raw.w;
+            const u32x4_t fa = lookup8(tb, wd);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) acc[0][j] = mfma32<DT>(fa, g.x[j][ks], acc[0][j]);
+        }
+    };
+    if (w0 < w1) {
+        int64_t st = w0;
+        for (; st + 3 <= w1; st += 3) {
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                compute(g[b]);
+                load(g[b], cl(st + b + 3));
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+            if (st + b < w1) compute(g[b]);
+    }
+
+    // fixed-order tree reduction of the waves' tiles through LDS (wave v += wave v + half,
+    // halving), then wave 0's epilogue
+#pragma unroll
+    for (int half = NW / 2; half >= 1; half /= 2) {
+        if (wave >= half && wave < 2 * half) {
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    s_red[wave - half][j * 4 + q][lane] =
+                        (float4_t){acc[0][j][4 * q], acc[0][j][4 * q + 1], acc[0][j][4 * q + 2],
+                                   acc[0][j][4 * q + 3]};
+        }
+        __syncthreads();
+        if (wave < half) {
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4_t t = s_red[wave][j * 4 + q][lane];
+                    acc[0][j][4 * q] += t.x;
+                    acc[0][j][4 * q + 1] += t.y;
+                    acc[0][j][4 * q + 2] += t.z;
+                    acc[0][j][4 * q + 3] += t.w;
+                }
+        }
+        if (half > 1) __syncthreads();
+    }
+    if (wave == 0) {
+        epilogue<DT, 1, MT>(a, acc, p0, w.rows, a.seg_off[seg], 0, split);
+    }
+}
+
 template <int DT, int BP, int BM, int WP, int WM>
 __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     constexpr int NT = WP * WM * 64;
@@ -638,13 +774,13 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
     __shared__ float s_code2[kMaxSeg][256];
 
-    const int64_t bid = blockIdx.x;
-    const int split = static_cast<int>(bid % a.splits);
-    const int64_t tile = bid / a.splits;
-    const int64_t p0 = (tile / a.m_tiles) * BP;
-    const int64_t m0 = (tile % a.m_tiles) * BM;
+    const int split = blockIdx.y;
+    const uint32_t tile = blockIdx.x;
+    const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
+    const int64_t p0 = static_cast<int64_t>(tile / mtl) * BP;
+    const int64_t m0 = static_cast<int64_t>(tile % mtl) * BM;
     const int64_t K = a.K;
-    const int64_t per = (a.total_steps + a.splits - 1) / a.splits;
+    const int64_t per = a.per_split;
     const int64_t s0 = split * per;
     const int64_t s1 = s0 + per < a.total_steps ? s0 + per : a.total_steps;
 
@@ -773,32 +909,65 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
 }
 
 // Split reduction: out[m][c] = sum_s partial[s][m][c] (+bias[c]) (+out if accumulate).
+// out[m][c] = sum_s partial[s][m][c] (+ bias[c]) (+ out[m][c]) in split order (deterministic).
+// Grid: x = groups of 1024 columns (4 per thread), y = rows (grid-stride).
 template <int DT>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial, int splits,
                                                            int64_t M, int64_t n_out,
                                                            const uint16_t *bias, uint16_t *out,
-                                                           int64_t ld_out, int accumulate) {
+                                                           int64_t ld_out, int accumulate,
+                                                           int vec) {
+    const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (c0 >= n_out) return;
     const int64_t total = M * n_out;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * 256) {
-        const int64_t m = i / n_out, c = i % n_out;
-        float v = 0.f;
-        for (int s = 0; s < splits; ++s) v += partial[s * total + i];
-        if (bias) v += to_f32<DT>(bias[c]);
-        uint16_t *dst = out + m * ld_out + c;
-        if (accumulate) v += to_f32<DT>(*dst);
-        *dst = from_f32<DT>(v);
+    const int nc = n_out - c0 < 4 ? static_cast<int>(n_out - c0) : 4;
+    for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+        const int64_t base = m * n_out + c0;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (vec && nc == 4) {
+            for (int s = 0; s < splits; ++s) {
+                const float4_t t = *reinterpret_cast<const float4_t *>(partial + s * total + base);
+                v[0] += t.x;
+                v[1] += t.y;
+                v[2] += t.z;
+                v[3] += t.w;
+            }
+        } else {
+            for (int s = 0; s < splits; ++s)
+                for (int q = 0; q < nc; ++q) v[q] += partial[s * total + base + q];
+        }
+        uint16_t *dst = out + m * ld_out + c0;
+        for (int q = 0; q < nc; ++q) {
+            if (bias) v[q] += to_f32<DT>(bias[c0 + q]);
+            if (accumulate) v[q] += to_f32<DT>(dst[q]);
+        }
+        if (vec && nc == 4) {
+            u32x2_t o;
+            o.x = pack2<DT>(v[0], v[1]);
+            o.y = pack2<DT>(v[2], v[3]);
+            *reinterpret_cast<u32x2_t *>(dst) = o;
+        } else {
+            for (int q = 0; q < nc; ++q) dst[q] = from_f32<DT>(v[q]);
+        }
     }
 }
 
 // ------------------------------------------------------------------------------ host side
 
 struct Plan {
-    int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves
+    int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves, 2: small-M path
     int bp, bm;
     int splits;
     int64_t tiles;
+    int waves;     // small-M path: waves per workgroup
 };
+
+// The small-M forward path takes M <= kGemvMaxM (32 x 1 or 2 activation rows per MFMA
+// B operand).  Its workgroups own 32 weight rows and their share of the reduction, spread over
+// 16 waves (8 with two activation fragments) while there are at most as many workgroups as
+// CUs, else 4 waves with several steps each.  Long reductions over few row tiles are split over
+// workgroups.
+constexpr int64_t kGemvMaxM = 64;
 
 constexpr int kCUs = 256;
 
@@ -864,7 +1033,7 @@ Plan make_plan(int64_t big, int64_t small, int64_t steps, int64_t out_elems) {
             if (s > 1 && (s - 1) * per >= steps) break;  // no empty split
             const double c = plan_cost(cfg, tiles, s, steps, out_elems);
             if (best.splits == 0 || c < best_cost) {
-                best = Plan{cfg, cfg == 0 ? 256 : 128, cfg == 0 ? 256 : 128, s, tiles};
+                best = Plan{cfg, cfg == 0 ? 256 : 128, cfg == 0 ? 256 : 128, s, tiles, 0};
                 best_cost = c;
             }
         }
@@ -872,7 +1041,30 @@ Plan make_plan(int64_t big, int64_t small, int64_t steps, int64_t out_elems) {
     return best;
 }
 
+Plan plan_gemv(int64_t m, const nf4_weight *ws, int nw) {
+    int64_t tiles = 0;
+    for (int i = 0; i < nw; ++i) tiles += (ws[i].rows + 31) / 32;
+    const int64_t steps = ws[0].cols / BR;
+    const int mt = m <= 32 ? 1 : 2;
+    int waves = tiles > kCUs ? 4 : 16;
+    while (waves > 4 && waves > steps) waves /= 2;
+    if (mt == 2 && waves > 8) waves = 8;  // two activation fragments need more than 128 VGPRs
+    // few row tiles and a long reduction: split it over workgroups (fp32 partials + the
+    // fixed-order reduction) so that more CUs dequantize, keeping >= 2 steps per wave
+    int64_t splits = 1;
+    if (tiles < kCUs / 2) {
+        splits = kCUs / tiles;
+        const int64_t by_steps = steps / (2 * waves);
+        if (splits > by_steps) splits = by_steps;
+        if (splits > kMaxSplits) splits = kMaxSplits;
+        if (splits < 1) splits = 1;
+        while (splits > 1 && (splits - 1) * ((steps + splits - 1) / splits) >= steps) --splits;
+    }
+    return Plan{2, 32, 32 * mt, static_cast<int>(splits), tiles, waves};
+}
+
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
+    if (m <= kGemvMaxM) return plan_gemv(m, ws, nw);
     int64_t big = 0, small = 0;
     for (int i = 0; i < nw; ++i) {
         big += (ws[i].rows + 255) / 256;
@@ -896,8 +1088,18 @@ Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
 
 template <int DT>
 int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
-    const dim3 grid(static_cast<unsigned>(p.tiles * p.splits));
-    if (p.cfg == 0)
+    const dim3 grid(static_cast<unsigned>(p.tiles), static_cast<unsigned>(p.splits));
+    if (p.cfg == 2) {
+        const dim3 block(p.waves * 64);
+        if (p.bm == 32) {
+            if (p.waves == 16) hipLaunchKernelGGL((gemv_kernel<DT, 1, 16>), grid, block, 0, st, g);
+            else if (p.waves == 8) hipLaunchKernelGGL((gemv_kernel<DT, 1, 8>), grid, block, 0, st, g);
+            else hipLaunchKernelGGL((gemv_kernel<DT, 1, 4>), grid, block, 0, st, g);
+        } else {
+            if (p.waves >= 8) hipLaunchKernelGGL((gemv_kernel<DT, 2, 8>), grid, dim3(512), 0, st, g);
+            else hipLaunchKernelGGL((gemv_kernel<DT, 2, 4>), grid, block, 0, st, g);
+        }
+    } else if (p.cfg == 0)
         hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
     else
         hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2>), grid, dim3(256), 0, st, g);
@@ -906,7 +1108,7 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
 
 template <int DT>
 int launch_dx(const GemmArgs &g, const Plan &p, hipStream_t st) {
-    const dim3 grid(static_cast<unsigned>(p.tiles * p.splits));
+    const dim3 grid(static_cast<unsigned>(p.tiles), static_cast<unsigned>(p.splits));
     if (p.cfg == 0)
         hipLaunchKernelGGL((dx_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
     else
@@ -916,12 +1118,14 @@ int launch_dx(const GemmArgs &g, const Plan &p, hipStream_t st) {
 
 template <int DT>
 int launch_reduce(const GemmArgs &g, int splits, hipStream_t st) {
-    const int64_t total = g.M * g.n_out;
-    int64_t blocks = (total + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(split_reduce_kernel<DT>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       st, g.partial, splits, g.M, g.n_out, g.bias,
-                       static_cast<uint16_t *>(g.out), g.ld_out, g.accumulate);
+    const int64_t cols = (g.n_out + 1023) / 1024;
+    const int64_t rows = g.M < 65535 ? g.M : 65535;
+    const int vec = g.n_out % 4 == 0 && g.ld_out % 4 == 0 && aligned(g.out, 8) &&
+                    aligned(g.partial, 16);
+    hipLaunchKernelGGL(split_reduce_kernel<DT>,
+                       dim3(static_cast<unsigned>(cols), static_cast<unsigned>(rows)), dim3(256),
+                       0, st, g.partial, splits, g.M, g.n_out, g.bias,
+                       static_cast<uint16_t *>(g.out), g.ld_out, g.accumulate, vec);
     return status_of(hipGetLastError());
 }
 
@@ -981,6 +1185,7 @@ extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_w
     for (int i = 0; i < nw; ++i) g.vec_out = g.vec_out && (g.seg_off[i] % 4 == 0);
     const Plan p = plan_fwd(m, ws, nw);
     g.splits = p.splits;
+    g.per_split = (g.K / BR + p.splits - 1) / p.splits;
     const int64_t bp = p.bp, bm = p.bm;
     g.m_tiles = (m + bm - 1) / bm;
     g.tile_start[0] = 0;
@@ -1040,6 +1245,7 @@ extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_
     g.step_start[0] = 0;
     for (int i = 0; i < nw; ++i) g.step_start[i + 1] = g.step_start[i] + (ws[i].rows + BR - 1) / BR;
     g.total_steps = g.step_start[nw];
+    g.per_split = (g.total_steps + p.splits - 1) / p.splits;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (p.splits > 1) {
         const size_t need = static_cast<size_t>(p.splits) * m * g.K * sizeof(float);

@@ -53,16 +53,20 @@ constexpr int kMaxRank = 64;
 // out[m][j] = scale * sum_k act[m][k] * W(j, k) on v_mfma_f32_16x16x32, where
 //   W(j, k) = w[j * K + k]    (B_LAYOUT false: LoRA A [rank, K], for t = xd A^T)
 //   W(j, k) = w[k * rank + j] (B_LAYOUT true:  LoRA B [N, rank], for da = s dY B).
-// A workgroup owns 16 rows m; its 4 waves split the reduction and add their 16 x 16 partial
-// tiles through LDS in a fixed order.  MFMA A operand = W (rows j), B operand = act (cols m).
+// A workgroup owns 16 rows m; its 16 waves split the reduction (short per-wave ranges keep
+// many loads in flight, also when M is a handful of tokens) and add their 16 x 16 partial tiles
+// through LDS in a fixed order.  MFMA A operand = W (rows j), B operand = act (cols m).
+constexpr int kRowdotWaves = 16;
+
 template <int DT, bool B_LAYOUT>
-__global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t *act, int64_t m, int64_t k,
-                                                     int64_t ld, const uint16_t *w, int rank,
-                                                     float scale, uint16_t *out, int vec) {
-    __shared__ float4_t red[4][64];
+__global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(
+    const uint16_t *act, int64_t m, int64_t k, int64_t ld, const uint16_t *w, int rank,
+    float scale, uint16_t *out, int vec) {
+    __shared__ float4_t red[kRowdotWaves][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16;
-    const int64_t kc = ((k + 127) / 128) * 32;  // per-wave share of k, a multiple of 32
+    // per-wave share of k, a multiple of 32
+    const int64_t kc = ((k + 32 * kRowdotWaves - 1) / (32 * kRowdotWaves)) * 32;
     const int64_t kb = wave * kc;
     const int64_t ke = kb + kc < k ? kb + kc : k;
     const int col = lane & 15, kq = (lane >> 4) * 8;
@@ -85,7 +89,8 @@ __global__ __launch_bounds__(256) void rowdot_kernel(const uint16_t *act, int64_
         red[wave][lane] = acc;
         __syncthreads();
         if (wave == 0) {
-            const float4_t s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+            float4_t s = red[0][lane];
+            for (int v = 1; v < kRowdotWaves; ++v) s += red[v][lane];
             const int64_t mm = m0 + (lane & 15);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -155,27 +160,37 @@ __global__ __launch_bounds__(256) void wgrad_partial_kernel(const uint16_t *u, i
     }
 }
 
+// out = scale * sum over chunks of part[chunk][p][j] ([p, rank], or [rank, p] transposed).
+// Thread i owns output element i of the stored layout (coalesced stores); four independent
+// partial sums over chunks c = 0, 1, 2, 3 mod 4 keep four loads in flight and are added in a
+// fixed order (deterministic).
 __global__ __launch_bounds__(256) void wgrad_final_kernel(const float *part, int chunks, int64_t p,
                                                           int rank, float scale, float *out,
                                                           int transpose_out) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= p * rank) return;
-    float s = 0.f;
-    for (int c = 0; c < chunks; ++c) s += part[c * p * rank + i];
-    const int64_t col = i / rank, j = i % rank;
-    if (transpose_out) out[j * p + col] = s * scale;
-    else out[i] = s * scale;
+    // 32-bit index arithmetic (p * rank < 2^31 is checked on the host)
+    const uint32_t ui = static_cast<uint32_t>(i), up = static_cast<uint32_t>(p);
+    const int64_t src = transpose_out ? static_cast<int64_t>(ui % up) * rank + ui / up : i;
+    const int64_t stride = p * rank;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    int c = 0;
+    for (; c + 4 <= chunks; c += 4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s[q] += part[(c + q) * stride + src];
+    }
+    for (int q = 0; c < chunks; ++c, ++q) s[q] += part[c * stride + src];
+    out[i] = ((s[0] + s[1]) + (s[2] + s[3])) * scale;
 }
 
-// Element i of a [rows, cols] grid stride loop; row-strided operands.
+// Grid: x = column groups of 256, y = rows (grid-stride); row-strided operands.
 template <int DT>
 __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const uint16_t *gate, const uint16_t *up,
                                                          int64_t ld_gu, uint16_t *out, int64_t ld_h,
                                                          int64_t rows, int64_t cols) {
-    const int64_t n = rows * cols;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * 256) {
-        const int64_t r = i / cols, c = i % cols;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (c >= cols) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
         const float g = ld1<DT>(gate + r * ld_gu + c), u = ld1<DT>(up + r * ld_gu + c);
         const float sig = 1.0f / (1.0f + __expf(-g));
         out[r * ld_h + c] = st1<DT>(g * sig * u);
@@ -187,10 +202,9 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t *grad, i
                                                          const uint16_t *gate, const uint16_t *up,
                                                          int64_t ld_gu, uint16_t *dgate,
                                                          uint16_t *dup, int64_t rows, int64_t cols) {
-    const int64_t n = rows * cols;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * 256) {
-        const int64_t r = i / cols, c = i % cols;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (c >= cols) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
         const float d = ld1<DT>(grad + r * ld_h + c);
         const float g = ld1<DT>(gate + r * ld_gu + c), u = ld1<DT>(up + r * ld_gu + c);
         const float sig = 1.0f / (1.0f + __expf(-g));
@@ -222,16 +236,24 @@ __global__ __launch_bounds__(256) void zero_kernel(float *out, int64_t n) {
         out[i] = 0.f;
 }
 
+// x: column groups of 256; y: rows, at most 4096 workgroup rows (grid-stride beyond).
+dim3 grid_2d(int64_t rows, int64_t cols) {
+    const int64_t x = (cols + 255) / 256;
+    const int64_t y = rows < 4096 ? rows : 4096;
+    return dim3(static_cast<unsigned>(x), static_cast<unsigned>(y < 1 ? 1 : y));
+}
+
 int grid_for(int64_t n) {
     int64_t b = (n + 255) / 256;
     return static_cast<int>(b > 16384 ? 16384 : (b < 1 ? 1 : b));
 }
 
 // Rows of M per wgrad workgroup: about 512 workgroups over the (64-column p tile x chunk) grid,
-// in multiples of the 32-row step.
+// at most 32 chunks, in multiples of the 32-row step.
 int64_t wgrad_rows_per_chunk(int64_t m, int64_t p) {
     const int64_t p_tiles = (p + 63) / 64;
     int64_t chunks = 512 / p_tiles;
+    if (chunks > 32) chunks = 32;  // the final sum reads every chunk's partial per output
     if (chunks < 1) chunks = 1;
     int64_t rows = (m + chunks - 1) / chunks;
     rows = ((rows + 31) / 32) * 32;
@@ -265,11 +287,11 @@ extern "C" int nf4_lora_xa(const void *xd, int64_t m, int64_t k, int64_t ldx, co
     auto s = static_cast<hipStream_t>(stream);
     auto A = static_cast<const uint16_t *>(xd);
     if (dtype == NF4_BF16)
-        hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, false>), grid, dim3(256), 0, s, A, m, k, ldx,
+        hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, false>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, k, ldx,
                            static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t),
                            vec);
     else
-        hipLaunchKernelGGL((rowdot_kernel<NF4_F16, false>), grid, dim3(256), 0, s, A, m, k, ldx,
+        hipLaunchKernelGGL((rowdot_kernel<NF4_F16, false>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, k, ldx,
                            static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t),
                            vec);
     return status_of(hipGetLastError());
@@ -287,11 +309,11 @@ extern "C" int nf4_lora_da(const void *dy, int64_t m, int64_t n, int64_t lddy, c
     auto s = static_cast<hipStream_t>(stream);
     auto A = static_cast<const uint16_t *>(dy);
     if (dtype == NF4_BF16)
-        hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, true>), grid, dim3(256), 0, s, A, m, n, lddy,
+        hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, true>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, n, lddy,
                            static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da),
                            vec);
     else
-        hipLaunchKernelGGL((rowdot_kernel<NF4_F16, true>), grid, dim3(256), 0, s, A, m, n, lddy,
+        hipLaunchKernelGGL((rowdot_kernel<NF4_F16, true>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, n, lddy,
                            static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da),
                            vec);
     return status_of(hipGetLastError());
@@ -320,7 +342,7 @@ extern "C" int nf4_lora_wgrad(const void *u, int64_t m, int64_t p, int64_t ldu, 
     if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
     const int64_t rows = wgrad_rows_per_chunk(m, p);
     const int64_t chunks = (m + rows - 1) / rows;
-    if (chunks > 65535 || (p + 63) / 64 > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
+    if (chunks > 65535 || p * rank >= (int64_t(1) << 31)) return NF4_ERR_UNSUPPORTED;
     float *part = static_cast<float *>(workspace);
     const dim3 grid(static_cast<unsigned>((p + 63) / 64), static_cast<unsigned>(chunks),
                     static_cast<unsigned>((rank + 15) / 16));
@@ -352,10 +374,10 @@ extern "C" int nf4_swiglu_fwd(const void *gate, const void *up, int64_t ld_gu, v
     auto u = static_cast<const uint16_t *>(up);
     auto o = static_cast<uint16_t *>(out);
     if (dtype == NF4_BF16)
-        hipLaunchKernelGGL(swiglu_fwd_kernel<NF4_BF16>, dim3(grid_for(n)), dim3(256), 0, s, g, u,
+        hipLaunchKernelGGL(swiglu_fwd_kernel<NF4_BF16>, grid_2d(rows, cols), dim3(256), 0, s, g, u,
                            ld_gu, o, ld_h, rows, cols);
     else
-        hipLaunchKernelGGL(swiglu_fwd_kernel<NF4_F16>, dim3(grid_for(n)), dim3(256), 0, s, g, u,
+        hipLaunchKernelGGL(swiglu_fwd_kernel<NF4_F16>, grid_2d(rows, cols), dim3(256), 0, s, g, u,
                            ld_gu, o, ld_h, rows, cols);
     return status_of(hipGetLastError());
 }
@@ -374,11 +396,11 @@ extern "C" int nf4_swiglu_bwd(const void *grad, int64_t ld_h, const void *gate, 
     auto dg = static_cast<uint16_t *>(dgate);
     auto du = static_cast<uint16_t *>(dup);
     if (dtype == NF4_BF16)
-        hipLaunchKernelGGL(swiglu_bwd_kernel<NF4_BF16>, dim3(grid_for(n)), dim3(256), 0, s, d, ld_h,
-                           g, u, ld_gu, dg, du, rows, cols);
+        hipLaunchKernelGGL(swiglu_bwd_kernel<NF4_BF16>, grid_2d(rows, cols), dim3(256), 0, s, d,
+                           ld_h, g, u, ld_gu, dg, du, rows, cols);
     else
-        hipLaunchKernelGGL(swiglu_bwd_kernel<NF4_F16>, dim3(grid_for(n)), dim3(256), 0, s, d, ld_h,
-                           g, u, ld_gu, dg, du, rows, cols);
+        hipLaunchKernelGGL(swiglu_bwd_kernel<NF4_F16>, grid_2d(rows, cols), dim3(256), 0, s, d,
+                           ld_h, g, u, ld_gu, dg, du, rows, cols);
     return status_of(hipGetLastError());
 }
 

@@ -4,6 +4,8 @@ nonzero status.  No arithmetic happens here."""
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -44,6 +46,23 @@ def dequant(weights, dtype=torch.float16, out: torch.Tensor | None = None) -> to
                                   stream_of(out))
     check(st, "nf4_dequant_multi")
     return out
+
+
+def dequant_batch(weights, dtype=torch.float16, outs=None) -> list:
+    """Each weight dequantized into its own [rows, cols] tensor, all in one launch
+    (nf4_dequant_batch, at most 8 weights)."""
+    packed0 = weights[0][0]
+    _check_device(packed0)
+    if outs is None:
+        outs = [torch.empty(tuple(int(d) for d in qs.shape), dtype=dtype, device=packed0.device)
+                for _, qs in weights]
+    arr = _descs(weights)
+    ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    st = load().nf4_dequant_batch(arr, len(weights), ptrs,
+                                  _code(dtype, (torch.float16, torch.bfloat16, torch.float32)),
+                                  stream_of(outs[0]))
+    check(st, "nf4_dequant_batch")
+    return outs
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor | None:

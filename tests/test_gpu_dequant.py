@@ -120,3 +120,25 @@ def test_round_to_nearest_even_ties(cuda):
         ref = o.dequantize(packed.numpy(), st, dt)
         ref = torch.from_numpy(ref.view(np.int16) if dt == "bf16" else ref.view(np.int16))
         assert torch.equal(_bits(out), ref), dt
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+def test_batch_bit_exact(cuda, dt):
+    """One launch, seven weights of a layer (different shapes) into separate outputs; then a
+    batch with an unaligned output (general path)."""
+    from solution import kernels
+
+    banner("dequant batch", dt)
+    shapes = [(192, 128), (64, 128), (64, 128), (128, 128), (320, 128), (320, 128), (128, 320)]
+    ws = [random_weight(n, k, seed=400 + i, dev=cuda) for i, (n, k) in enumerate(shapes)]
+    outs = kernels.dequant_batch(ws, DT[dt])
+    for (p, qs), out in zip(ws, outs):
+        assert torch.equal(_bits(out).reshape(-1), _oracle(p, qs, dt).reshape(-1))
+    odd = [random_weight(n, k, seed=500 + n, dev=cuda, blocksize=bs)
+           for n, k, bs in ((5, 12, 4), (33, 64, 64), (3, 100, 128))]
+    buf = torch.zeros(5 * 12 + 1 + 33 * 64 + 3 * 100, dtype=DT[dt], device=cuda)
+    views = [buf[1:61].view(5, 12), buf[61:61 + 2112].view(33, 64), buf[2173:2473].view(3, 100)]
+    kernels.dequant_batch(odd, DT[dt], outs=views)
+    for (p, qs), out in zip(odd, views):
+        assert torch.equal(_bits(out).reshape(-1), _oracle(p, qs, dt).reshape(-1))
+    assert _bits(buf[:1]).item() == 0

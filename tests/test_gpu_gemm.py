@@ -168,3 +168,35 @@ def test_bias_grad_and_swiglu(cuda):
     (o.silu(gg) * uu).backward(grad.float().cpu())
     torch.testing.assert_close(d[:, :96].float().cpu(), gg.grad, rtol=5e-3, atol=5e-3)
     torch.testing.assert_close(d[:, 96:].float().cpu(), uu.grad, rtol=5e-3, atol=5e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 8, 33, 64])
+def test_small_m_stacked_bias_lora(cuda, m, dtype):
+    """The small-M forward path (decode regime): stacked segments whose row counts are not
+    multiples of its 32-row tiles, bias, LoRA on two segments; and a long reduction (split over
+    workgroups, fp32 partials + fixed-order reduction)."""
+    from solution import kernels
+
+    banner("gemm small-M", m, dtype)
+    dt = "bf16" if dtype == torch.bfloat16 else "f16"
+    k, r, s = 640, 16, 2.0
+    segs = [random_weight(n, k, seed=300 + n, dev=cuda) for n in (100, 36, 28)]
+    w = torch.cat([oracle_w16(p, q, dt) for p, q in segs])
+    x = _x(m, k, 31, cuda, dtype)
+    bias = _x(1, 164, 32, cuda, dtype, std=0.5).view(-1)
+    g = torch.Generator().manual_seed(33)
+    a0 = ((torch.rand(r, k, generator=g) * 2 - 1) / k ** 0.5).to(dtype).to(cuda)
+    a2 = ((torch.rand(r, k, generator=g) * 2 - 1) / k ** 0.5).to(dtype).to(cuda)
+    b0 = (torch.randn(100, r, generator=g) * 0.05).to(dtype).to(cuda)
+    b2 = (torch.randn(28, r, generator=g) * 0.05).to(dtype).to(cuda)
+    t0, t2 = kernels.lora_xa(x, a0), kernels.lora_xa(x, a2)
+    loras = [kernels.make_lora(0, r, s, t=t0, b=b0), kernels.make_lora(2, r, s, t=t2, b=b2)]
+    y = kernels.linear_fwd(x, segs, bias, loras)
+    ref = o.linear_fwd(x, w, bias, [(0, 100, x, a0, b0, s), (136, 28, x, a2, b2, s)])
+    assert_rel(y, ref, what="small-M stacked fwd")
+    # long K: 140 steps, split over workgroups
+    pd, qd = random_weight(96, 8960, seed=301, dev=cuda)
+    xd = _x(m, 8960, 34, cuda, dtype)
+    assert_rel(kernels.linear_fwd(xd, [(pd, qd)]), o.linear_fwd(xd, oracle_w16(pd, qd, dt)),
+               what="small-M long K")
