@@ -71,9 +71,15 @@ struct GemmArgs {
     void *out;
     int64_t ld_out;
     int64_t n_out;                // forward: sum rows; dx: K
-    float *partial;               // split workspace [splits][M][n_out] or null
-    int splits;                   // reduction splits = gridDim.y
+    // Tiles [0, tail_start) run whole; tiles [tail_start, tiles) (a column range
+    // [tail_col0, n_out) of the output) are split over `splits` workgroups each, which write
+    // fp32 partials [splits][M][tail_cols] for the fixed-order reduction kernel.
+    float *partial;               // split workspace or null
+    int splits;
     int64_t per_split;            // reduction steps per split (host-computed: no divisions)
+    int64_t tail_start;
+    int64_t tail_col0;
+    int64_t tail_cols;
     int64_t m_tiles;
     int64_t p_tiles;              // dx: tiles along K
     int64_t total_steps;          // dx: sum of step counts
@@ -118,6 +124,22 @@ __device__ __forceinline__ int seg_of_step(const GemmArgs &a, int64_t t) {
     for (int i = 1; i < kMaxSeg; ++i)
         if (i < a.nseg && t >= a.step_start[i]) s = i;
     return s;
+}
+
+// Workgroup -> (tile, split, number of splits of that tile): 1-D grid of tail_start whole
+// tiles followed by `splits` workgroups per tail tile.  32-bit arithmetic.
+struct BlockTile {
+    int64_t tile;
+    int split;
+    int nsplit;
+};
+
+__device__ __forceinline__ BlockTile block_tile(const GemmArgs &a) {
+    const uint32_t b = blockIdx.x;
+    const uint32_t ts = static_cast<uint32_t>(a.tail_start);
+    if (b < ts) return BlockTile{b, 0, 1};
+    const uint32_t r = b - ts, sp = static_cast<uint32_t>(a.splits);
+    return BlockTile{static_cast<int64_t>(ts + r / sp), static_cast<int>(r % sp), a.splits};
 }
 
 // The raw absmax inputs of block b, fetched with the packed bytes; rebuilt later by absmax_val.
@@ -305,11 +327,11 @@ __device__ __forceinline__ u32x4_t gather8(const uint16_t *src, int64_t stride, 
 }
 
 // Epilogue: lane holds C[p .. p+3][m] for each (i, j, r4).  Writes either fp32 partials
-// (split mode) or final values (+bias, +existing for accumulate) in DT.
+// (a split tail tile) or final values (+bias, +existing for accumulate) in DT.
 template <int DT, int TP, int TM>
 __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP][TM],
                                          int64_t p_base, int64_t p_end, int64_t col_off,
-                                         int64_t m_base, int split) {
+                                         int64_t m_base, int split, bool to_partial) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
@@ -325,8 +347,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
                 float v[4] = {acc[i][j][r4 * 4 + 0], acc[i][j][r4 * 4 + 1],
                               acc[i][j][r4 * 4 + 2], acc[i][j][r4 * 4 + 3]};
                 const bool full = p + 4 <= p_end;
-                if (a.partial) {
-                    float *dst = a.partial + (static_cast<int64_t>(split) * a.M + m) * a.n_out + col;
+                if (to_partial) {
+                    float *dst = a.partial + (static_cast<int64_t>(split) * a.M + m) * a.tail_cols +
+                                 (col - a.tail_col0);
                     if (full) {
                         *reinterpret_cast<float4_t *>(dst) = (float4_t){v[0], v[1], v[2], v[3]};
                     } else {
@@ -497,10 +520,11 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
     __shared__ float s_code2[256];
 
-    // grid: x = tile (segments in order, m fastest), y = reduction split.  32-bit tile
-    // arithmetic: 64-bit divisions are long scalar sequences the whole CU waits on.
-    const int split = blockIdx.y;
-    const int64_t tile = blockIdx.x;
+    // tiles: segments in order, m fastest.  32-bit tile arithmetic: 64-bit divisions are long
+    // scalar sequences the whole CU waits on.
+    const BlockTile bt = block_tile(a);
+    const int split = bt.split;
+    const int64_t tile = bt.tile;
     const int seg = seg_of_tile(a, tile);
     const uint32_t local = static_cast<uint32_t>(tile - a.tile_start[seg]);
     const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
@@ -509,7 +533,7 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const DevWeight w = a.w[seg];  // by value: kept in registers for the whole loop
     const int64_t K = a.K;
     const int64_t steps = K / BR;
-    const int64_t per = a.per_split;
+    const int64_t per = bt.nsplit > 1 ? a.per_split : steps;
     const int64_t s0 = split * per;
     const int64_t s1 = s0 + per < steps ? s0 + per : steps;
 
@@ -603,7 +627,7 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
         if (st < s1) mma_step<DT, TP, TM>(acc, sW[0], sA[0], wp * (BP / WP), wm * (BM / WM));
     }
     epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), w.rows, a.seg_off[seg],
-                         m0 + wm * (BM / WM), split);
+                         m0 + wm * (BM / WM), split, bt.nsplit > 1);
 }
 
 // ------------------------------------------------------------------- small-M forward path
@@ -624,14 +648,15 @@ void gemv_kernel(const GemmArgs a) {
     __shared__ float s_code2[256];
     __shared__ float4_t s_red[NW / 2][MT * 4][64];
 
-    const int split = blockIdx.y;
-    const int64_t tile = blockIdx.x;
+    const BlockTile bt = block_tile(a);
+    const int split = bt.split;
+    const int64_t tile = bt.tile;
     const int seg = seg_of_tile(a, tile);
     const int64_t p0 = (tile - a.tile_start[seg]) * 32;
     const DevWeight w = a.w[seg];
     const int64_t K = a.K;
     const int64_t steps = K / BR;
-    const int64_t per = a.per_split;
+    const int64_t per = bt.nsplit > 1 ? a.per_split : steps;
     const int64_t s0 = split * per;
     const int64_t s1 = s0 + per < steps ? s0 + per : steps;
     // wave-uniform: the step range below lives in scalar registers
@@ -761,7 +786,7 @@ void gemv_kernel(const GemmArgs a) {
         if (half > 1) __syncthreads();
     }
     if (wave == 0) {
-        epilogue<DT, 1, MT>(a, acc, p0, w.rows, a.seg_off[seg], 0, split);
+        epilogue<DT, 1, MT>(a, acc, p0, w.rows, a.seg_off[seg], 0, split, bt.nsplit > 1);
     }
 }
 
@@ -774,13 +799,14 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
     __shared__ float s_code2[kMaxSeg][256];
 
-    const int split = blockIdx.y;
-    const uint32_t tile = blockIdx.x;
+    const BlockTile bt = block_tile(a);
+    const int split = bt.split;
+    const uint32_t tile = static_cast<uint32_t>(bt.tile);
     const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
     const int64_t p0 = static_cast<int64_t>(tile / mtl) * BP;
     const int64_t m0 = static_cast<int64_t>(tile % mtl) * BM;
     const int64_t K = a.K;
-    const int64_t per = a.per_split;
+    const int64_t per = bt.nsplit > 1 ? a.per_split : a.total_steps;
     const int64_t s0 = split * per;
     const int64_t s1 = s0 + per < a.total_steps ? s0 + per : a.total_steps;
 
@@ -905,15 +931,16 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
                                         [](int) {});
         }
     }
-    epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), K, 0, m0 + wm * (BM / WM), split);
+    epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), K, 0, m0 + wm * (BM / WM), split,
+                         bt.nsplit > 1);
 }
 
-// Split reduction: out[m][c] = sum_s partial[s][m][c] (+bias[c]) (+out if accumulate).
-// out[m][c] = sum_s partial[s][m][c] (+ bias[c]) (+ out[m][c]) in split order (deterministic).
-// Grid: x = groups of 1024 columns (4 per thread), y = rows (grid-stride).
+// Split reduction over the tail columns [col0, col0 + n_out):
+// out[m][col0 + c] = sum_s partial[s][m][c] (+ bias[col0 + c]) (+ out[m][col0 + c]) in split
+// order (deterministic).  Grid: x = groups of 1024 columns (4 per thread), y = rows.
 template <int DT>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial, int splits,
-                                                           int64_t M, int64_t n_out,
+                                                           int64_t M, int64_t n_out, int64_t col0,
                                                            const uint16_t *bias, uint16_t *out,
                                                            int64_t ld_out, int accumulate,
                                                            int vec) {
@@ -921,6 +948,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial,
     if (c0 >= n_out) return;
     const int64_t total = M * n_out;
     const int nc = n_out - c0 < 4 ? static_cast<int>(n_out - c0) : 4;
+    if (bias) bias += col0;
+    out += col0;
     for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
         const int64_t base = m * n_out + c0;
         float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -957,9 +986,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial,
 struct Plan {
     int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves, 2: small-M path
     int bp, bm;
-    int splits;
+    int splits;    // reduction splits of the tail tiles
     int64_t tiles;
     int waves;     // small-M path: waves per workgroup
+    int64_t tail_start;  // first split tile (tiles before it run whole)
+
+    int64_t blocks() const { return tail_start + (tiles - tail_start) * splits; }
 };
 
 // The small-M forward path takes M <= kGemvMaxM (32 x 1 or 2 activation rows per MFMA
@@ -1013,28 +1045,47 @@ int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const n
 // MFMA, which the step times already contain.
 constexpr int kMaxSplits = 16;
 
-double plan_cost(int cfg, int64_t tiles, int splits, int64_t steps, int64_t out_elems) {
-    const int64_t blocks = tiles * splits;
+// Time of a plan: workgroups are dispatched in order into `slots` places (one per CU for the
+// 256x256 tile, two for 128x128).  The whole tiles run in rounds; the split tail tiles' shorter
+// workgroups first fill the places the last whole round leaves free, then run in rounds of
+// their own.  A split also pays the fp32 partial round trip and the reduction launch.
+double plan_cost(int cfg, int64_t tiles, int64_t mt, int64_t tail_start, int splits,
+                 int64_t steps, int64_t m) {
     const int64_t slots = cfg == 0 ? kCUs : 2 * kCUs;
+    const int64_t bp = cfg == 0 ? 256 : 128;
+    const int64_t full = splits > 1 ? tail_start : tiles;
+    const int64_t tail_blocks = splits > 1 ? (tiles - tail_start) * splits : 0;
+    const double t_step = cfg == 0 ? 2.6 : (full + tail_blocks <= kCUs ? 1.35 : 1.6);
     const int64_t per = (steps + splits - 1) / splits;
-    const double t_step = cfg == 0 ? 2.6 : (blocks <= kCUs ? 1.35 : 1.6);
-    double c = double((blocks + slots - 1) / slots) * double(per) * t_step + 1.0;
-    if (splits > 1) c += 2.0 * double(splits) * double(out_elems) * 4.0 / 5.0e6 + 12.0;
+    const int64_t rounds = (full + slots - 1) / slots;
+    double c = double(rounds) * double(steps) * t_step + 1.0;
+    const int64_t free_slots = rounds * slots - full;
+    if (tail_blocks > free_slots)
+        c += double((tail_blocks - free_slots + slots - 1) / slots) * double(per) * t_step;
+    if (splits > 1) {
+        const double tail_cols = double((tiles - tail_start) / mt) * double(bp);
+        c += 2.0 * double(splits) * double(m) * tail_cols * 4.0 / 5.0e6 + 12.0;
+    }
     return c;
 }
 
-Plan make_plan(int64_t big, int64_t small, int64_t steps, int64_t out_elems) {
+Plan make_plan(int64_t m, int64_t big, int64_t small, int64_t steps) {
     Plan best{};
     double best_cost = 0.0;
     for (int cfg = 0; cfg < 2; ++cfg) {
         const int64_t tiles = cfg == 0 ? big : small;
+        const int64_t mt = (m + (cfg == 0 ? 255 : 127)) / (cfg == 0 ? 256 : 128);
         for (int s = 1; s <= kMaxSplits; ++s) {
             const int64_t per = (steps + s - 1) / s;
             if (s > 1 && (s - 1) * per >= steps) break;  // no empty split
-            const double c = plan_cost(cfg, tiles, s, steps, out_elems);
-            if (best.splits == 0 || c < best_cost) {
-                best = Plan{cfg, cfg == 0 ? 256 : 128, cfg == 0 ? 256 : 128, s, tiles, 0};
-                best_cost = c;
+            // the split tail starts at a p-tile boundary (a column range of the output)
+            for (int64_t ts = 0; ts < (s > 1 ? tiles : 1); ts += mt) {
+                const double c = plan_cost(cfg, tiles, mt, ts, s, steps, m);
+                if (best.splits == 0 || c < best_cost) {
+                    best = Plan{cfg, cfg == 0 ? 256 : 128, cfg == 0 ? 256 : 128, s, tiles, 0,
+                                s > 1 ? ts : tiles};
+                    best_cost = c;
+                }
             }
         }
     }
@@ -1060,7 +1111,7 @@ Plan plan_gemv(int64_t m, const nf4_weight *ws, int nw) {
         if (splits < 1) splits = 1;
         while (splits > 1 && (splits - 1) * ((steps + splits - 1) / splits) >= steps) --splits;
     }
-    return Plan{2, 32, 32 * mt, static_cast<int>(splits), tiles, waves};
+    return Plan{2, 32, 32 * mt, static_cast<int>(splits), tiles, waves, splits > 1 ? 0 : tiles};
 }
 
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
@@ -1072,9 +1123,7 @@ Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
     }
     big *= (m + 255) / 256;
     small *= (m + 127) / 128;
-    int64_t n = 0;
-    for (int i = 0; i < nw; ++i) n += ws[i].rows;
-    return make_plan(big, small, ws[0].cols / BR, m * n);
+    return make_plan(m, big, small, ws[0].cols / BR);
 }
 
 Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
@@ -1083,12 +1132,12 @@ Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
     const int64_t K = ws[0].cols;
     const int64_t big = ((K + 255) / 256) * ((m + 255) / 256);
     const int64_t small = ((K + 127) / 128) * ((m + 127) / 128);
-    return make_plan(big, small, steps, m * K);
+    return make_plan(m, big, small, steps);
 }
 
 template <int DT>
 int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
-    const dim3 grid(static_cast<unsigned>(p.tiles), static_cast<unsigned>(p.splits));
+    const dim3 grid(static_cast<unsigned>(p.blocks()));
     if (p.cfg == 2) {
         const dim3 block(p.waves * 64);
         if (p.bm == 32) {
@@ -1108,7 +1157,7 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
 
 template <int DT>
 int launch_dx(const GemmArgs &g, const Plan &p, hipStream_t st) {
-    const dim3 grid(static_cast<unsigned>(p.tiles), static_cast<unsigned>(p.splits));
+    const dim3 grid(static_cast<unsigned>(p.blocks()));
     if (p.cfg == 0)
         hipLaunchKernelGGL((dx_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
     else
@@ -1118,15 +1167,34 @@ int launch_dx(const GemmArgs &g, const Plan &p, hipStream_t st) {
 
 template <int DT>
 int launch_reduce(const GemmArgs &g, int splits, hipStream_t st) {
-    const int64_t cols = (g.n_out + 1023) / 1024;
+    const int64_t cols = (g.tail_cols + 1023) / 1024;
     const int64_t rows = g.M < 65535 ? g.M : 65535;
-    const int vec = g.n_out % 4 == 0 && g.ld_out % 4 == 0 && aligned(g.out, 8) &&
-                    aligned(g.partial, 16);
+    const int vec = g.tail_cols % 4 == 0 && g.tail_col0 % 4 == 0 && g.ld_out % 4 == 0 &&
+                    aligned(g.out, 8) && aligned(g.partial, 16);
     hipLaunchKernelGGL(split_reduce_kernel<DT>,
                        dim3(static_cast<unsigned>(cols), static_cast<unsigned>(rows)), dim3(256),
-                       0, st, g.partial, splits, g.M, g.n_out, g.bias,
+                       0, st, g.partial, splits, g.M, g.tail_cols, g.tail_col0, g.bias,
                        static_cast<uint16_t *>(g.out), g.ld_out, g.accumulate, vec);
     return status_of(hipGetLastError());
+}
+
+// First output column of the split tail tiles (output columns: the segments' rows stacked; each
+// segment's tiles run p-tile by p-tile with m fastest).
+int64_t fwd_tail_col0(const Plan &p, int64_t m, const nf4_weight *ws, int nw) {
+    const int64_t mt = (m + p.bm - 1) / p.bm;
+    int64_t t = 0, col = 0;
+    for (int i = 0; i < nw; ++i) {
+        const int64_t tiles_i = ((ws[i].rows + p.bp - 1) / p.bp) * mt;
+        if (p.tail_start < t + tiles_i) return col + ((p.tail_start - t) / mt) * p.bp;
+        t += tiles_i;
+        col += ws[i].rows;
+    }
+    return col;
+}
+
+int64_t dx_tail_col0(const Plan &p, int64_t m) {
+    const int64_t mt = (m + p.bm - 1) / p.bm;
+    return (p.tail_start / mt) * p.bp;
 }
 
 }  // namespace
@@ -1138,7 +1206,7 @@ extern "C" size_t nf4_linear_fwd_workspace(int64_t m, const nf4_weight *ws, int 
     if (p.splits <= 1) return 0;
     int64_t n = 0;
     for (int i = 0; i < nw; ++i) n += ws[i].rows;
-    return static_cast<size_t>(p.splits) * m * n * sizeof(float);
+    return static_cast<size_t>(p.splits) * m * (n - fwd_tail_col0(p, m, ws, nw)) * sizeof(float);
 }
 
 extern "C" size_t nf4_linear_dx_workspace(int64_t m, const nf4_weight *ws, int nw, int dtype) {
@@ -1146,7 +1214,7 @@ extern "C" size_t nf4_linear_dx_workspace(int64_t m, const nf4_weight *ws, int n
     if (!ws || nw < 1 || nw > kMaxSeg || m <= 0) return 0;
     const Plan p = plan_dx(m, ws, nw);
     if (p.splits <= 1) return 0;
-    return static_cast<size_t>(p.splits) * m * ws[0].cols * sizeof(float);
+    return static_cast<size_t>(p.splits) * m * (ws[0].cols - dx_tail_col0(p, m)) * sizeof(float);
 }
 
 extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_weight *ws, int nw,
@@ -1192,8 +1260,11 @@ extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_w
     for (int i = 0; i < nw; ++i)
         g.tile_start[i + 1] = g.tile_start[i] + ((ws[i].rows + bp - 1) / bp) * g.m_tiles;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    g.tail_start = p.tail_start;
+    g.tail_col0 = p.splits > 1 ? fwd_tail_col0(p, m, ws, nw) : n_out;
+    g.tail_cols = n_out - g.tail_col0;
     if (p.splits > 1) {
-        const size_t need = static_cast<size_t>(p.splits) * m * n_out * sizeof(float);
+        const size_t need = static_cast<size_t>(p.splits) * m * g.tail_cols * sizeof(float);
         if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
         g.partial = static_cast<float *>(workspace);
     }
@@ -1247,8 +1318,11 @@ extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_
     g.total_steps = g.step_start[nw];
     g.per_split = (g.total_steps + p.splits - 1) / p.splits;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    g.tail_start = p.tail_start;
+    g.tail_col0 = p.splits > 1 ? dx_tail_col0(p, m) : g.K;
+    g.tail_cols = g.K - g.tail_col0;
     if (p.splits > 1) {
-        const size_t need = static_cast<size_t>(p.splits) * m * g.K * sizeof(float);
+        const size_t need = static_cast<size_t>(p.splits) * m * g.tail_cols * sizeof(float);
         if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
         g.partial = static_cast<float *>(workspace);
     }
