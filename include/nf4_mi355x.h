@@ -144,6 +144,33 @@ int nf4_lora_wgrad(const void *u, int64_t m, int64_t p, int64_t ldu, const void 
                    void *workspace, size_t workspace_bytes, void *stream);
 size_t nf4_lora_wgrad_workspace(int64_t m, int64_t p, int rank);
 
+/* Several LoRA side products in one launch (q and v adapters of a layer).  A job names the
+ * rows of its [M, cols] operand (already at the job's first column: da and dB read column
+ * ranges of the stacked q|k|v gradient), the small operand and the output. */
+#define NF4_MAX_LORA_JOBS 4
+typedef struct nf4_lora_job {
+    const void *in;        /* [M, cols] operand rows, `ld` elements apart */
+    int64_t ld;
+    int64_t cols;          /* xa: K; da: N; wgrad: P */
+    const void *w;         /* xa: A [rank, cols]; da: B [cols, rank]; wgrad: V [M, rank] */
+    void *out;             /* xa / da: [M, rank] GEMM dtype; wgrad: fp32 [cols, rank] or
+                            * [rank, cols] (transpose_out) */
+    float scale;
+    int32_t transpose_out; /* wgrad only */
+} nf4_lora_job;
+
+/* t_j = in_j @ A_j^T for every job (nf4_lora_xa per job: layer.py:875, 877). */
+int nf4_lora_xa_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
+                      void *stream);
+/* da_j = scale_j * in_j @ B_j for every job (nf4_lora_da per job: layer.py:1074-1078). */
+int nf4_lora_da_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
+                      void *stream);
+/* out_j = scale_j * in_j^T @ V_j for every job, one partial and one final launch
+ * (nf4_lora_wgrad per job: layer.py:1075-1076, 1080-1081). */
+int nf4_lora_wgrad_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
+                         void *workspace, size_t workspace_bytes, void *stream);
+size_t nf4_lora_wgrad_multi_workspace(const nf4_lora_job *jobs, int njobs, int64_t m, int rank);
+
 /* -------------------------------------------------------------------------- small helpers */
 
 /* out[rows, cols] = silu(gate) * up, and its gradient (the SwiGLU step between the gate/up and

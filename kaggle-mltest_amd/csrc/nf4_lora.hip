@@ -50,6 +50,25 @@ __device__ __forceinline__ u32x4_t frag8(const uint16_t *src, int64_t stride, in
 
 constexpr int kMaxRank = 64;
 
+// One LoRA side product of a launch (the C ABI's nf4_lora_job plus host-computed layout).
+struct Job {
+    const uint16_t *in;   // rowdot: act rows; wgrad: U rows (already at their column offset)
+    int64_t ld;
+    int64_t cols;         // rowdot: reduction length; wgrad: P
+    const uint16_t *w;    // rowdot: A [rank, cols] or B [cols, rank]; wgrad: V [M, rank]
+    void *out;
+    float scale;
+    int transpose;        // wgrad: out is [rank, P]
+    int vec;              // rowdot: bit 0 act rows 16-byte loadable, bit 1 A rows; wgrad: U rows
+    int64_t part_off;     // wgrad: float offset of this job's partials in the workspace
+    int64_t out_start;    // wgrad: first output element of this job in the final grid
+};
+
+struct Jobs {
+    Job j[NF4_MAX_LORA_JOBS];
+    int n;
+};
+
 // out[m][j] = scale * sum_k act[m][k] * W(j, k) on v_mfma_f32_16x16x32, where
 //   W(j, k) = w[j * K + k]    (B_LAYOUT false: LoRA A [rank, K], for t = xd A^T)
 //   W(j, k) = w[k * rank + j] (B_LAYOUT true:  LoRA B [N, rank], for da = s dY B).
@@ -59,10 +78,13 @@ constexpr int kMaxRank = 64;
 constexpr int kRowdotWaves = 16;
 
 template <int DT, bool B_LAYOUT>
-__global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(
-    const uint16_t *act, int64_t m, int64_t k, int64_t ld, const uint16_t *w, int rank,
-    float scale, uint16_t *out, int vec) {
+__global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jobs, int64_t m,
+                                                                     int rank) {
     __shared__ float4_t red[kRowdotWaves][64];
+    const Job &jb = jobs.j[blockIdx.y];
+    const uint16_t *act = jb.in, *w = jb.w;
+    const int64_t k = jb.cols, ld = jb.ld;
+    uint16_t *out = static_cast<uint16_t *>(jb.out);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16;
     // per-wave share of k, a multiple of 32
@@ -81,8 +103,8 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(
             if (lim > 0) {
                 if (j < rank)
                     fa = B_LAYOUT ? frag8(w + kk * rank + j, rank, lim, false)
-                                  : frag8(w + j * k + kk, 1, lim, (vec & 2) != 0);
-                if (row < m) fb = frag8(act + row * ld + kk, 1, lim, (vec & 1) != 0);
+                                  : frag8(w + j * k + kk, 1, lim, (jb.vec & 2) != 0);
+                if (row < m) fb = frag8(act + row * ld + kk, 1, lim, (jb.vec & 1) != 0);
             }
             acc = mfma16<DT>(fa, fb, acc);
         }
@@ -95,7 +117,7 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int jj = j0 + (lane >> 4) * 4 + q;
-                if (mm < m && jj < rank) out[mm * rank + jj] = st1<DT>(s[q] * scale);
+                if (mm < m && jj < rank) out[mm * rank + jj] = st1<DT>(s[q] * jb.scale);
             }
         }
         __syncthreads();
@@ -107,18 +129,24 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(
 // for a 64-column tile of p (4 waves x 16) and one 16-wide tile of j (blockIdx.z).  Both
 // operands are reduced over m, so each 32-row step is staged in LDS transposed ([p][m], [j][m])
 // and the MFMA fragments are contiguous 16-byte LDS reads.
+// Grid: x = 64-column p tiles (of the widest job), y = row chunks, z = job x 16-wide j tiles.
 template <int DT>
-__global__ __launch_bounds__(256) void wgrad_partial_kernel(const uint16_t *u, int64_t m, int64_t p,
-                                                            int64_t ldu, const uint16_t *v, int rank,
-                                                            int64_t rows_per_chunk, float *part,
-                                                            int vec_u) {
+__global__ __launch_bounds__(256) void wgrad_partial_kernel(const Jobs jobs, int64_t m, int rank,
+                                                            int64_t rows_per_chunk, float *ws) {
     constexpr int SR = 40;  // LDS row: 32 m + 8 pad (80 bytes)
     __shared__ __attribute__((aligned(16))) uint16_t sU[64 * SR];
     __shared__ __attribute__((aligned(16))) uint16_t sV[16 * SR];
+    const int jtiles = (rank + 15) / 16;
+    const Job &jb = jobs.j[blockIdx.z / jtiles];
+    const uint16_t *u = jb.in, *v = jb.w;
+    const int64_t p = jb.cols, ldu = jb.ld;
+    const int vec_u = jb.vec;
+    float *part = ws + jb.part_off;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 64;
+    if (p0 >= p) return;  // a narrower job than the grid (uniform per workgroup)
     const int64_t chunk = blockIdx.y;
-    const int j0 = blockIdx.z * 16;
+    const int j0 = (blockIdx.z % jtiles) * 16;
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -160,18 +188,25 @@ __global__ __launch_bounds__(256) void wgrad_partial_kernel(const uint16_t *u, i
     }
 }
 
-// out = scale * sum over chunks of part[chunk][p][j] ([p, rank], or [rank, p] transposed).
-// Thread i owns output element i of the stored layout (coalesced stores); four independent
-// partial sums over chunks c = 0, 1, 2, 3 mod 4 keep four loads in flight and are added in a
-// fixed order (deterministic).
-__global__ __launch_bounds__(256) void wgrad_final_kernel(const float *part, int chunks, int64_t p,
-                                                          int rank, float scale, float *out,
-                                                          int transpose_out) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= p * rank) return;
+// out = scale * sum over chunks of part[chunk][p][j] ([p, rank], or [rank, p] transposed), for
+// every job: the grid covers all jobs' outputs back to back.  Thread i owns output element i of
+// its job's stored layout (coalesced stores); four independent partial sums over chunks
+// c = 0, 1, 2, 3 mod 4 keep four loads in flight and are added in a fixed order (deterministic).
+__global__ __launch_bounds__(256) void wgrad_final_kernel(const Jobs jobs, const float *ws,
+                                                          int chunks, int rank, int64_t total) {
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (g >= total) return;
+    int ji = 0;
+#pragma unroll
+    for (int q = 1; q < NF4_MAX_LORA_JOBS; ++q)
+        if (q < jobs.n && g >= jobs.j[q].out_start) ji = q;
+    const Job &jb = jobs.j[ji];
+    const float *part = ws + jb.part_off;
+    const int64_t p = jb.cols;
+    const int64_t i = g - jb.out_start;
     // 32-bit index arithmetic (p * rank < 2^31 is checked on the host)
     const uint32_t ui = static_cast<uint32_t>(i), up = static_cast<uint32_t>(p);
-    const int64_t src = transpose_out ? static_cast<int64_t>(ui % up) * rank + ui / up : i;
+    const int64_t src = jb.transpose ? static_cast<int64_t>(ui % up) * rank + ui / up : i;
     const int64_t stride = p * rank;
     float s[4] = {0.f, 0.f, 0.f, 0.f};
     int c = 0;
@@ -180,7 +215,7 @@ __global__ __launch_bounds__(256) void wgrad_final_kernel(const float *part, int
         for (int q = 0; q < 4; ++q) s[q] += part[(c + q) * stride + src];
     }
     for (int q = 0; c < chunks; ++c, ++q) s[q] += part[c * stride + src];
-    out[i] = ((s[0] + s[1]) + (s[2] + s[3])) * scale;
+    static_cast<float *>(jb.out)[i] = ((s[0] + s[1]) + (s[2] + s[3])) * jb.scale;
 }
 
 // Grid: x = column groups of 256, y = rows (grid-stride); row-strided operands.
@@ -275,92 +310,165 @@ extern "C" const char *nf4_status_string(int status) {
     }
 }
 
+namespace {
+
+int check_jobs(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype) {
+    if ((dtype != NF4_F16 && dtype != NF4_BF16) || m < 0 || rank < 1 || rank > kMaxRank)
+        return NF4_ERR_ARG;
+    if (!jobs || njobs < 1 || njobs > NF4_MAX_LORA_JOBS) return NF4_ERR_ARG;
+    for (int i = 0; i < njobs; ++i) {
+        const nf4_lora_job &j = jobs[i];
+        if (j.cols < 0 || j.ld < j.cols || !j.out) return NF4_ERR_ARG;
+        if (m > 0 && j.cols > 0 && (!j.in || !j.w)) return NF4_ERR_ARG;
+    }
+    if ((m + 15) / 16 > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
+    return NF4_OK;
+}
+
+Jobs to_jobs(const nf4_lora_job *jobs, int njobs) {
+    Jobs J = {};
+    J.n = njobs;
+    for (int i = 0; i < njobs; ++i) {
+        const nf4_lora_job &j = jobs[i];
+        J.j[i] = Job{static_cast<const uint16_t *>(j.in), j.ld, j.cols,
+                     static_cast<const uint16_t *>(j.w), j.out, j.scale, j.transpose_out != 0, 0,
+                     0, 0};
+    }
+    return J;
+}
+
+// xa (A rows contiguous) or da (B columns strided) for every job, one launch.
+template <bool B_LAYOUT>
+int rowdot_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
+                 void *stream) {
+    int st = check_jobs(jobs, njobs, m, rank, dtype);
+    if (st != NF4_OK || m == 0) return st;
+    Jobs J = to_jobs(jobs, njobs);
+    for (int i = 0; i < njobs; ++i) {
+        Job &j = J.j[i];
+        j.vec = (j.ld % 8 == 0 && aligned(j.in, 16) ? 1 : 0) |
+                (!B_LAYOUT && j.cols % 8 == 0 && aligned(j.w, 16) ? 2 : 0);
+    }
+    const dim3 grid(static_cast<unsigned>((m + 15) / 16), static_cast<unsigned>(njobs));
+    auto s = static_cast<hipStream_t>(stream);
+    if (dtype == NF4_BF16)
+        hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, B_LAYOUT>), grid, dim3(kRowdotWaves * 64), 0,
+                           s, J, m, rank);
+    else
+        hipLaunchKernelGGL((rowdot_kernel<NF4_F16, B_LAYOUT>), grid, dim3(kRowdotWaves * 64), 0,
+                           s, J, m, rank);
+    return status_of(hipGetLastError());
+}
+
+// Layout of the wgrad partials: rows per chunk from the widest job, jobs back to back.
+struct WgradLayout {
+    int64_t rows, chunks, maxp, floats, outputs;
+};
+
+WgradLayout wgrad_layout(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, Jobs *J) {
+    WgradLayout L = {};
+    for (int i = 0; i < njobs; ++i) L.maxp = jobs[i].cols > L.maxp ? jobs[i].cols : L.maxp;
+    L.rows = wgrad_rows_per_chunk(m, L.maxp > 0 ? L.maxp : 1);
+    L.chunks = (m + L.rows - 1) / L.rows;
+    for (int i = 0; i < njobs; ++i) {
+        if (J) {
+            J->j[i].part_off = L.floats;
+            J->j[i].out_start = L.outputs;
+        }
+        L.floats += L.chunks * jobs[i].cols * rank;
+        L.outputs += jobs[i].cols * rank;
+    }
+    return L;
+}
+
+}  // namespace
+
+extern "C" int nf4_lora_xa_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank,
+                                 int dtype, void *stream) {
+    return rowdot_multi<false>(jobs, njobs, m, rank, dtype, stream);
+}
+
+extern "C" int nf4_lora_da_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank,
+                                 int dtype, void *stream) {
+    return rowdot_multi<true>(jobs, njobs, m, rank, dtype, stream);
+}
+
 extern "C" int nf4_lora_xa(const void *xd, int64_t m, int64_t k, int64_t ldx, const void *a,
                            int rank, void *t, int dtype, void *stream) {
-    if ((dtype != NF4_F16 && dtype != NF4_BF16) || m < 0 || k < 0 || rank < 1 || rank > kMaxRank)
-        return NF4_ERR_ARG;
-    if (m == 0) return NF4_OK;
-    if (!xd || !a || !t || ldx < k) return NF4_ERR_ARG;
-    if ((m + 15) / 16 > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
-    const dim3 grid(static_cast<unsigned>((m + 15) / 16));
-    const int vec = (ldx % 8 == 0 && aligned(xd, 16) ? 1 : 0) | (k % 8 == 0 && aligned(a, 16) ? 2 : 0);
-    auto s = static_cast<hipStream_t>(stream);
-    auto A = static_cast<const uint16_t *>(xd);
-    if (dtype == NF4_BF16)
-        hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, false>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, k, ldx,
-                           static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t),
-                           vec);
-    else
-        hipLaunchKernelGGL((rowdot_kernel<NF4_F16, false>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, k, ldx,
-                           static_cast<const uint16_t *>(a), rank, 1.0f, static_cast<uint16_t *>(t),
-                           vec);
-    return status_of(hipGetLastError());
+    if (m > 0 && (!xd || !a || !t)) return NF4_ERR_ARG;
+    const nf4_lora_job j = {xd, ldx, k, a, t, 1.0f, 0};
+    return nf4_lora_xa_multi(&j, 1, m, rank, dtype, stream);
 }
 
 extern "C" int nf4_lora_da(const void *dy, int64_t m, int64_t n, int64_t lddy, const void *b,
                            int rank, float scale, void *da, int dtype, void *stream) {
-    if ((dtype != NF4_F16 && dtype != NF4_BF16) || m < 0 || n < 0 || rank < 1 || rank > kMaxRank)
-        return NF4_ERR_ARG;
-    if (m == 0) return NF4_OK;
-    if (!dy || !b || !da || lddy < n) return NF4_ERR_ARG;
-    if ((m + 15) / 16 > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
-    const dim3 grid(static_cast<unsigned>((m + 15) / 16));
-    const int vec = lddy % 8 == 0 && aligned(dy, 16) ? 1 : 0;
+    if (m > 0 && (!dy || !b || !da)) return NF4_ERR_ARG;
+    const nf4_lora_job j = {dy, lddy, n, b, da, scale, 0};
+    return nf4_lora_da_multi(&j, 1, m, rank, dtype, stream);
+}
+
+extern "C" size_t nf4_lora_wgrad_multi_workspace(const nf4_lora_job *jobs, int njobs, int64_t m,
+                                                 int rank) {
+    if (!jobs || njobs < 1 || njobs > NF4_MAX_LORA_JOBS || m <= 0 || rank <= 0) return 0;
+    return static_cast<size_t>(wgrad_layout(jobs, njobs, m, rank, nullptr).floats) *
+           sizeof(float);
+}
+
+extern "C" int nf4_lora_wgrad_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank,
+                                    int dtype, void *workspace, size_t workspace_bytes,
+                                    void *stream) {
+    int st = check_jobs(jobs, njobs, m, rank, dtype);
+    if (st != NF4_OK) return st;
     auto s = static_cast<hipStream_t>(stream);
-    auto A = static_cast<const uint16_t *>(dy);
+    Jobs J = to_jobs(jobs, njobs);
+    const WgradLayout L = wgrad_layout(jobs, njobs, m, rank, &J);
+    if (L.outputs == 0) return NF4_OK;
+    for (int i = 0; i < njobs; ++i)
+        if (jobs[i].cols * rank >= (int64_t(1) << 31)) return NF4_ERR_UNSUPPORTED;
+    if (m == 0) {  // zero gradients, by fill kernels (no memset nodes if the call is captured)
+        for (int i = 0; i < njobs; ++i) {
+            const int64_t n = jobs[i].cols * rank;
+            if (n == 0) continue;
+            hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n)), dim3(256), 0, s,
+                               static_cast<float *>(jobs[i].out), n);
+        }
+        return status_of(hipGetLastError());
+    }
+    const size_t need = static_cast<size_t>(L.floats) * sizeof(float);
+    if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
+    if (L.chunks > 65535 || static_cast<int64_t>(njobs) * ((rank + 15) / 16) > 65535)
+        return NF4_ERR_UNSUPPORTED;
+    for (int i = 0; i < njobs; ++i) {
+        Job &j = J.j[i];
+        j.vec = j.ld % 8 == 0 && aligned(j.in, 16) ? 1 : 0;
+    }
+    float *ws = static_cast<float *>(workspace);
+    const dim3 grid(static_cast<unsigned>((L.maxp + 63) / 64), static_cast<unsigned>(L.chunks),
+                    static_cast<unsigned>(njobs * ((rank + 15) / 16)));
     if (dtype == NF4_BF16)
-        hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, true>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, n, lddy,
-                           static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da),
-                           vec);
+        hipLaunchKernelGGL(wgrad_partial_kernel<NF4_BF16>, grid, dim3(256), 0, s, J, m, rank,
+                           L.rows, ws);
     else
-        hipLaunchKernelGGL((rowdot_kernel<NF4_F16, true>), grid, dim3(kRowdotWaves * 64), 0, s, A, m, n, lddy,
-                           static_cast<const uint16_t *>(b), rank, scale, static_cast<uint16_t *>(da),
-                           vec);
+        hipLaunchKernelGGL(wgrad_partial_kernel<NF4_F16>, grid, dim3(256), 0, s, J, m, rank,
+                           L.rows, ws);
+    st = status_of(hipGetLastError());
+    if (st != NF4_OK) return st;
+    hipLaunchKernelGGL(wgrad_final_kernel, dim3(static_cast<unsigned>((L.outputs + 255) / 256)),
+                       dim3(256), 0, s, J, ws, static_cast<int>(L.chunks), rank, L.outputs);
     return status_of(hipGetLastError());
 }
 
 extern "C" size_t nf4_lora_wgrad_workspace(int64_t m, int64_t p, int rank) {
-    if (m <= 0 || p <= 0 || rank <= 0) return 0;
-    const int64_t rows = wgrad_rows_per_chunk(m, p);
-    const int64_t chunks = (m + rows - 1) / rows;
-    return static_cast<size_t>(chunks) * p * rank * sizeof(float);
+    const nf4_lora_job j = {nullptr, p, p, nullptr, nullptr, 1.0f, 0};
+    return nf4_lora_wgrad_multi_workspace(&j, 1, m, rank);
 }
 
 extern "C" int nf4_lora_wgrad(const void *u, int64_t m, int64_t p, int64_t ldu, const void *v,
                               int rank, float scale, float *out, int transpose_out, int dtype,
                               void *workspace, size_t workspace_bytes, void *stream) {
-    if ((dtype != NF4_F16 && dtype != NF4_BF16) || m < 0 || p < 0 || rank < 1 || rank > kMaxRank)
-        return NF4_ERR_ARG;
-    if (!out || (m > 0 && (!u || !v)) || ldu < p) return NF4_ERR_ARG;
-    auto s = static_cast<hipStream_t>(stream);
-    if (p == 0) return NF4_OK;
-    if (m == 0) {  // a fill kernel, not a memset node, so the call may be graph-captured
-        hipLaunchKernelGGL(zero_kernel, dim3(grid_for(p * rank)), dim3(256), 0, s, out, p * rank);
-        return status_of(hipGetLastError());
-    }
-    const size_t need = nf4_lora_wgrad_workspace(m, p, rank);
-    if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
-    const int64_t rows = wgrad_rows_per_chunk(m, p);
-    const int64_t chunks = (m + rows - 1) / rows;
-    if (chunks > 65535 || p * rank >= (int64_t(1) << 31)) return NF4_ERR_UNSUPPORTED;
-    float *part = static_cast<float *>(workspace);
-    const dim3 grid(static_cast<unsigned>((p + 63) / 64), static_cast<unsigned>(chunks),
-                    static_cast<unsigned>((rank + 15) / 16));
-    const int vec_u = ldu % 8 == 0 && aligned(u, 16) ? 1 : 0;
-    if (dtype == NF4_BF16)
-        hipLaunchKernelGGL(wgrad_partial_kernel<NF4_BF16>, grid, dim3(256), 0, s,
-                           static_cast<const uint16_t *>(u), m, p, ldu,
-                           static_cast<const uint16_t *>(v), rank, rows, part, vec_u);
-    else
-        hipLaunchKernelGGL(wgrad_partial_kernel<NF4_F16>, grid, dim3(256), 0, s,
-                           static_cast<const uint16_t *>(u), m, p, ldu,
-                           static_cast<const uint16_t *>(v), rank, rows, part, vec_u);
-    int st = status_of(hipGetLastError());
-    if (st != NF4_OK) return st;
-    hipLaunchKernelGGL(wgrad_final_kernel, dim3(static_cast<unsigned>((p * rank + 255) / 256)),
-                       dim3(256), 0, s, part, static_cast<int>(chunks), p, rank, scale, out,
-                       transpose_out);
-    return status_of(hipGetLastError());
+    if (!out || (m > 0 && p > 0 && (!u || !v))) return NF4_ERR_ARG;
+    const nf4_lora_job j = {u, ldu, p, v, out, scale, transpose_out};
+    return nf4_lora_wgrad_multi(&j, 1, m, rank, dtype, workspace, workspace_bytes, stream);
 }
 
 extern "C" int nf4_swiglu_fwd(const void *gate, const void *up, int64_t ld_gu, void *out,

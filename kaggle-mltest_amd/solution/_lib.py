@@ -46,6 +46,14 @@ class NF4Lora(ctypes.Structure):
 
 
 # name -> (restype, argtypes)
+class NF4LoraJob(ctypes.Structure):
+    """struct nf4_lora_job (include/nf4_mi355x.h), 48 bytes."""
+    _fields_ = [
+        ("in_", c_void_p), ("ld", c_int64), ("cols", c_int64), ("w", c_void_p), ("out", c_void_p),
+        ("scale", c_float), ("transpose_out", ctypes.c_int32),
+    ]
+
+
 _SIGNATURES = {
     "nf4_abi_version": (c_int, []),
     "nf4_status_string": (ctypes.c_char_p, [c_int]),
@@ -68,6 +76,14 @@ _SIGNATURES = {
     "nf4_lora_wgrad": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int, c_float,
                                c_void_p, c_int, c_int, c_void_p, c_size_t, c_void_p]),
     "nf4_lora_wgrad_workspace": (c_size_t, [c_int64, c_int64, c_int]),
+    "nf4_lora_xa_multi": (c_int, [ctypes.POINTER(NF4LoraJob), c_int, c_int64, c_int, c_int,
+                                  c_void_p]),
+    "nf4_lora_da_multi": (c_int, [ctypes.POINTER(NF4LoraJob), c_int, c_int64, c_int, c_int,
+                                  c_void_p]),
+    "nf4_lora_wgrad_multi": (c_int, [ctypes.POINTER(NF4LoraJob), c_int, c_int64, c_int, c_int,
+                                     c_void_p, c_size_t, c_void_p]),
+    "nf4_lora_wgrad_multi_workspace": (c_size_t, [ctypes.POINTER(NF4LoraJob), c_int, c_int64,
+                                                  c_int]),
     "nf4_swiglu_fwd": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64,
                                c_int, c_void_p]),
     "nf4_swiglu_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,

@@ -9,7 +9,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import DTYPE_CODE, NF4Lora, check, load, stream_of
+from ._lib import DTYPE_CODE, NF4Lora, NF4LoraJob, check, load, stream_of
 from .quant_state import weight_array, weight_desc
 
 GEMM_DTYPES = (torch.float16, torch.bfloat16)
@@ -209,3 +209,41 @@ def make_lora(seg: int, rank: int, scale: float, t=None, b=None, a=None, da=None
 
 __all__ = ["dequant", "linear_fwd", "linear_dx", "lora_xa", "lora_da", "lora_wgrad",
            "swiglu_fwd", "swiglu_bwd", "bias_grad", "make_lora", "GEMM_DTYPES", "_lib"]
+
+
+def lora_job(inp: torch.Tensor, w: torch.Tensor, out: torch.Tensor, scale: float = 1.0,
+             transpose_out: bool = False) -> NF4LoraJob:
+    """One job of the multi LoRA launches: `inp` [M, cols] (any row stride), `w` the small
+    operand, `out` the result; the tensors stay alive for the call (the caller keeps them)."""
+    _check_device(inp, w, out)
+    return NF4LoraJob(in_=inp.data_ptr(), ld=inp.stride(0), cols=inp.shape[1], w=w.data_ptr(),
+                      out=out.data_ptr(), scale=float(scale), transpose_out=int(transpose_out))
+
+
+def _jobs(jobs):
+    return (NF4LoraJob * len(jobs))(*jobs), len(jobs)
+
+
+def lora_xa_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor):
+    """t_j = in_j @ A_j^T for every job, one launch."""
+    arr, n = _jobs(jobs)
+    check(load().nf4_lora_xa_multi(arr, n, m, rank, _code(dtype), stream_of(stream_tensor)),
+          "nf4_lora_xa_multi")
+
+
+def lora_da_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor):
+    """da_j = scale_j * in_j @ B_j for every job, one launch."""
+    arr, n = _jobs(jobs)
+    check(load().nf4_lora_da_multi(arr, n, m, rank, _code(dtype), stream_of(stream_tensor)),
+          "nf4_lora_da_multi")
+
+
+def lora_wgrad_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor):
+    """out_j = scale_j * in_j^T @ V_j (fp32) for every job: one partial and one final launch."""
+    arr, n = _jobs(jobs)
+    lib = load()
+    nbytes = lib.nf4_lora_wgrad_multi_workspace(arr, n, m, rank)
+    ws = _workspace(nbytes, stream_tensor.device)
+    check(lib.nf4_lora_wgrad_multi(arr, n, m, rank, _code(dtype),
+                                   ws.data_ptr() if ws is not None else None, nbytes,
+                                   stream_of(stream_tensor)), "nf4_lora_wgrad_multi")

@@ -81,6 +81,17 @@ def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _run_jobs(fn, jobs, like):
+    """Run (rank, nf4_lora_job) jobs through a multi launch, grouped by rank, at most 4 per
+    launch (one launch for the q and v adapters of a layer)."""
+    by_rank = {}
+    for r, j in jobs:
+        by_rank.setdefault(r, []).append(j)
+    for r, js in by_rank.items():
+        for k in range(0, len(js), 4):
+            fn(js[k:k + 4], like.shape[0], r, like.dtype, like)
+
+
 class NF4Projection(torch.autograd.Function):
     """apply(x [M, K], bias or None, spec, A_0, B_0, A_1, B_1, ...) -> Y [M, sum rows]."""
 
@@ -88,13 +99,15 @@ class NF4Projection(torch.autograd.Function):
     def forward(ctx, x, bias, spec, *lora_params):
         dtype = x.dtype
         x = _aligned_rows(x)
-        structs, saved = [], []
+        structs, saved, jobs = [], [], []
         for ad, a, b in zip(spec.loras, lora_params[0::2], lora_params[1::2]):
             a16 = a.detach().to(dtype).contiguous()
             b16 = b.detach().to(dtype).contiguous()
-            t = kernels.lora_xa(x, a16)
+            t = torch.empty((x.shape[0], a16.shape[0]), dtype=dtype, device=x.device)
+            jobs.append((a16.shape[0], kernels.lora_job(x, a16, t)))
             structs.append(kernels.make_lora(ad.seg, a16.shape[0], ad.scale, t=t, b=b16))
             saved += [t, a16, b16]
+        _run_jobs(kernels.lora_xa_multi, jobs, x)  # t = x A^T for every adapter
         b = None if bias is None else bias.detach().to(dtype).contiguous()
         y = kernels.linear_fwd(x, spec.weights, b, structs)
         ctx.spec = spec
@@ -109,18 +122,26 @@ class NF4Projection(torch.autograd.Function):
         spec = ctx.spec
         dy = _aligned_rows(dy.to(x.dtype))
         offs = spec.offsets()
-        grads, structs = [], []
+        grads, structs, da_jobs, wg_jobs, pairs = [], [], [], [], []
         for i, ad in enumerate(spec.loras):
             t, a16, b16 = saved[3 * i: 3 * i + 3]
+            r = a16.shape[0]
             rows = int(spec.weights[ad.seg][1].shape[0])
             dy_s = dy[:, offs[ad.seg]: offs[ad.seg] + rows]
             if dy_s.data_ptr() % 16:
                 dy_s = dy_s.contiguous()
-            da = kernels.lora_da(dy_s, b16, ad.scale)
-            grad_b = kernels.lora_wgrad(dy_s, t, ad.scale, transpose_out=False)
-            grad_a = kernels.lora_wgrad(x, da, 1.0, transpose_out=True)
+            da = torch.empty((x.shape[0], r), dtype=x.dtype, device=x.device)
+            grad_b = torch.empty((rows, r), dtype=torch.float32, device=x.device)
+            grad_a = torch.empty((r, x.shape[1]), dtype=torch.float32, device=x.device)
+            da_jobs.append((r, kernels.lora_job(dy_s, b16, da, ad.scale)))
+            wg_jobs += [(r, kernels.lora_job(dy_s, t, grad_b, ad.scale)),
+                        (r, kernels.lora_job(x, da, grad_a, 1.0, transpose_out=True))]
+            pairs.append((grad_a, grad_b, dy_s))
+            structs.append(kernels.make_lora(ad.seg, r, ad.scale, a=a16, da=da))
+        _run_jobs(kernels.lora_da_multi, da_jobs, x)         # da = s dY_seg B
+        _run_jobs(kernels.lora_wgrad_multi, wg_jobs, x)      # dB = s dY_seg^T t, dA = da^T x
+        for i, (grad_a, grad_b, _) in enumerate(pairs):
             grads += [grad_a.to(ctx.param_dtypes[2 * i]), grad_b.to(ctx.param_dtypes[2 * i + 1])]
-            structs.append(kernels.make_lora(ad.seg, a16.shape[0], ad.scale, a=a16, da=da))
         dx = kernels.linear_dx(dy, spec.weights, structs) if ctx.needs_input_grad[0] else None
         dbias = kernels.bias_grad(dy) if ctx.has_bias and ctx.needs_input_grad[1] else None
         return (dx, dbias, None, *grads)

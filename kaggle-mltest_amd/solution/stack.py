@@ -9,9 +9,10 @@ layer reads fixed input buffers, so a step is exactly the projection work of the
 
 Every launch goes through the C ABI with argument arrays built once, on torch's current
 stream, in the order the reference runs them:
-  forward, per layer:  t_q = X A_q^T, t_v = X A_v^T; q|k|v (+bias, +LoRA); o; gate|up; down
-  backward, reversed:  dX down; dX gate|up; dX o; da_q, da_v; dB_q, dB_v, dA_q, dA_v;
-                       dX q|k|v (+LoRA)
+  forward, per layer:  t_q = X A_q^T and t_v = X A_v^T (one launch); q|k|v (+bias, +LoRA);
+                       o; gate|up; down
+  backward, reversed:  dX down; dX gate|up; dX o; da_q, da_v (one launch); dB_q, dB_v, dA_q,
+                       dA_v (one partial + one final launch); dX q|k|v (+LoRA)
 """
 
 from __future__ import annotations
@@ -110,6 +111,18 @@ class ProjectionStack:
                                       Lo(2, rank, self.scale, P(self.t_v), P(L["b_v"]), None, None))
             L["dx_loras"] = (Lo * 2)(Lo(0, rank, self.scale, None, None, P(L["a_q"]), P(self.da_q)),
                                      Lo(2, rank, self.scale, None, None, P(L["a_v"]), P(self.da_v)))
+            # the side products of both adapters, one launch each (nf4_lora_job arrays)
+            J, es = _lib.NF4LoraJob, self.dy_qkv.element_size()
+            dq, dv = P(self.dy_qkv), P(self.dy_qkv) + (h + kv) * es
+            nq = self.n_qkv
+            L["xa_jobs"] = (J * 2)(J(P(self.x), h, h, P(L["a_q"]), P(self.t_q), 1.0, 0),
+                                   J(P(self.x), h, h, P(L["a_v"]), P(self.t_v), 1.0, 0))
+            L["da_jobs"] = (J * 2)(J(dq, nq, h, P(L["b_q"]), P(self.da_q), self.scale, 0),
+                                   J(dv, nq, kv, P(L["b_v"]), P(self.da_v), self.scale, 0))
+            L["wg_jobs"] = (J * 4)(J(dq, nq, h, P(self.t_q), P(L["gb_q"]), self.scale, 0),
+                                   J(dv, nq, kv, P(self.t_v), P(L["gb_v"]), self.scale, 0),
+                                   J(P(self.x), h, h, P(self.da_q), P(L["ga_q"]), 1.0, 1),
+                                   J(P(self.x), h, h, P(self.da_v), P(L["ga_v"]), 1.0, 1))
             self.per_layer.append(L)
         self.ws = {}
         self.set_tokens(torch.tensor([0, max_tokens], dtype=torch.int32))
@@ -143,8 +156,7 @@ class ProjectionStack:
         for g, _ in GROUPS:
             need[g] = (lib.nf4_linear_fwd_workspace(m, L0[g], L0[g + "_n"], self.dt),
                        lib.nf4_linear_dx_workspace(m, L0[g], L0[g + "_n"], self.dt))
-        need["wgrad"] = (max(lib.nf4_lora_wgrad_workspace(m, p, self.rank)
-                             for p in (self.shape.hidden, self.shape.kv)), 0)
+        need["wgrad"] = (lib.nf4_lora_wgrad_multi_workspace(L0["wg_jobs"], 4, m, self.rank), 0)
         for key, (fb, db) in need.items():
             have = self.ws.get(key)
             if have is None or have[1] < fb or have[3] < db:
@@ -194,8 +206,7 @@ class ProjectionStack:
         ws = self.ws
         for li in (range(len(self.per_layer)) if layers is None else layers):
             L = self.per_layer[li]
-            self._chk(lib.nf4_lora_xa(P(self.x), m, h, h, P(L["a_q"]), r, P(self.t_q), dt, s), "xa")
-            self._chk(lib.nf4_lora_xa(P(self.x), m, h, h, P(L["a_v"]), r, P(self.t_v), dt, s), "xa")
+            self._chk(lib.nf4_lora_xa_multi(L["xa_jobs"], 2, m, r, dt, s), "xa")
             self._timed(ev, "fwd_qkv", lambda: lib.nf4_linear_fwd(
                 P(self.x), m, h, L["qkv"], 3, P(L["bias"]), L["fwd_loras"], 2, P(self.y_qkv), nq,
                 dt, P(ws["qkv"][0]), ws["qkv"][1], s))
@@ -215,8 +226,8 @@ class ProjectionStack:
         lib, dt, m = self.lib, self.dt, self.m
         s = torch.cuda.current_stream(self.dev).cuda_stream
         P = lambda t: t.data_ptr()  # noqa: E731
-        h, i, kv, nq, r = self.shape.hidden, self.shape.inter, self.shape.kv, self.n_qkv, self.rank
-        ws, es = self.ws, self.dy_qkv.element_size()
+        h, i, nq, r = self.shape.hidden, self.shape.inter, self.n_qkv, self.rank
+        ws = self.ws
         wg, wb = P(ws["wgrad"][0]), ws["wgrad"][1]
         order = reversed(range(len(self.per_layer))) if layers is None else layers
         for li in order:
@@ -230,19 +241,9 @@ class ProjectionStack:
             self._timed(ev, "dx_o", lambda: lib.nf4_linear_dx(
                 P(self.dy_o), m, h, L["o"], 1, None, 0, P(self.dx_o), h, 0, dt,
                 P(ws["o"][2]), ws["o"][3], s))
-            dq, dv = P(self.dy_qkv), P(self.dy_qkv) + (h + kv) * es
-            self._chk(lib.nf4_lora_da(dq, m, h, nq, P(L["b_q"]), r, self.scale, P(self.da_q),
-                                      dt, s), "da")
-            self._chk(lib.nf4_lora_da(dv, m, kv, nq, P(L["b_v"]), r, self.scale, P(self.da_v),
-                                      dt, s), "da")
-            self._chk(lib.nf4_lora_wgrad(dq, m, h, nq, P(self.t_q), r, self.scale, P(L["gb_q"]),
-                                         0, dt, wg, wb, s), "wgrad")
-            self._chk(lib.nf4_lora_wgrad(dv, m, kv, nq, P(self.t_v), r, self.scale, P(L["gb_v"]),
-                                         0, dt, wg, wb, s), "wgrad")
-            self._chk(lib.nf4_lora_wgrad(P(self.x), m, h, h, P(self.da_q), r, 1.0, P(L["ga_q"]),
-                                         1, dt, wg, wb, s), "wgrad")
-            self._chk(lib.nf4_lora_wgrad(P(self.x), m, h, h, P(self.da_v), r, 1.0, P(L["ga_v"]),
-                                         1, dt, wg, wb, s), "wgrad")
+            dq = P(self.dy_qkv)
+            self._chk(lib.nf4_lora_da_multi(L["da_jobs"], 2, m, r, dt, s), "da")
+            self._chk(lib.nf4_lora_wgrad_multi(L["wg_jobs"], 4, m, r, dt, wg, wb, s), "wgrad")
             self._timed(ev, "dx_qkv", lambda: lib.nf4_linear_dx(
                 dq, m, nq, L["qkv"], 3, L["dx_loras"], 2, P(self.dx_qkv), h, 0, dt,
                 P(ws["qkv"][2]), ws["qkv"][3], s))

@@ -48,11 +48,13 @@ def test_exports_in_shared_object():
 
 
 def test_struct_layouts_match_header():
-    from solution._lib import NF4Lora, NF4Weight
+    from solution._lib import NF4Lora, NF4LoraJob, NF4Weight
 
     assert ctypes.sizeof(NF4Weight) == 72
     assert NF4Weight.rows.offset == 48 and NF4Weight.blocksize2.offset == 68
     assert ctypes.sizeof(NF4Lora) == 48 and NF4Lora.t.offset == 16
+    assert ctypes.sizeof(NF4LoraJob) == 48 and NF4LoraJob.scale.offset == 40
+    assert NF4LoraJob.transpose_out.offset == 44
 
 
 def test_version_and_status_strings(lib):

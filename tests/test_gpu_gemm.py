@@ -200,3 +200,42 @@ def test_small_m_stacked_bias_lora(cuda, m, dtype):
     xd = _x(m, 8960, 34, cuda, dtype)
     assert_rel(kernels.linear_fwd(xd, [(pd, qd)]), o.linear_fwd(xd, oracle_w16(pd, qd, dt)),
                what="small-M long K")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_lora_multi_matches_single(cuda, dtype):
+    """The multi-job LoRA launches give the single-job results bit for bit (same kernels, same
+    order of arithmetic), with jobs on column ranges of a stacked gradient."""
+    from solution import kernels
+
+    banner("lora multi", dtype)
+    m, k, r = 300, 512, 16
+    x = _x(m, k, 41, cuda, dtype)
+    dy = _x(m, 768, 42, cuda, dtype, std=1e-3)
+    g = torch.Generator().manual_seed(43)
+    a = [((torch.rand(r, k, generator=g) * 2 - 1) / k ** 0.5).to(dtype).to(cuda) for _ in range(2)]
+    b = [(torch.randn(n, r, generator=g) * 0.05).to(dtype).to(cuda) for n in (512, 128)]
+    cols = [dy[:, :512], dy[:, 640:]]
+    t = [torch.empty(m, r, dtype=dtype, device=cuda) for _ in range(2)]
+    kernels.lora_xa_multi([kernels.lora_job(x, a[i], t[i]) for i in range(2)], m, r, dtype, x)
+    for i in range(2):
+        assert torch.equal(t[i], kernels.lora_xa(x, a[i]))
+    da = [torch.empty(m, r, dtype=dtype, device=cuda) for _ in range(2)]
+    kernels.lora_da_multi([kernels.lora_job(cols[i], b[i], da[i], 2.0) for i in range(2)], m, r,
+                          dtype, x)
+    for i in range(2):
+        assert torch.equal(da[i], kernels.lora_da(cols[i].contiguous(), b[i], 2.0))
+    gb = [torch.empty(n, r, dtype=torch.float32, device=cuda) for n in (512, 128)]
+    ga = [torch.empty(r, k, dtype=torch.float32, device=cuda) for _ in range(2)]
+    jobs = [kernels.lora_job(cols[i], t[i], gb[i], 2.0) for i in range(2)] + \
+        [kernels.lora_job(x, da[i], ga[i], 1.0, transpose_out=True) for i in range(2)]
+    kernels.lora_wgrad_multi(jobs, m, r, dtype, x)
+    for i in range(2):
+        ref_b = kernels.lora_wgrad(cols[i].contiguous(), t[i], 2.0, False)
+        ref_a = kernels.lora_wgrad(x, da[i], 1.0, True)
+        ga_o, gb_o = o.lora_grads(cols[i], x, a[i], b[i], 2.0)
+        assert_rel(gb[i], gb_o, mean_rel=3e-3 if dtype == torch.bfloat16 else 1e-3, what="dB")
+        assert_rel(ga[i], ga_o, mean_rel=3e-3 if dtype == torch.bfloat16 else 1e-3, what="dA")
+        # the multi launch reduces over the widest job's chunking: equal within fp32 rounding
+        torch.testing.assert_close(gb[i], ref_b, rtol=1e-5, atol=1e-7)
+        torch.testing.assert_close(ga[i], ref_a, rtol=1e-5, atol=1e-7)
