@@ -126,6 +126,15 @@ __device__ __forceinline__ int seg_of_step(const GemmArgs &a, int64_t t) {
     return s;
 }
 
+// A value known to be the same in every lane, kept in scalar registers (the compiler otherwise
+// can lose track through VALU-computed integer division and then wraps every buffer load that
+// uses it in a per-lane loop).
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Workgroup -> (tile, split, number of splits of that tile): 1-D grid of tail_start whole
 // tiles followed by `splits` workgroups per tail tile.  32-bit arithmetic.
 struct BlockTile {
@@ -139,7 +148,8 @@ __device__ __forceinline__ BlockTile block_tile(const GemmArgs &a) {
     const uint32_t ts = static_cast<uint32_t>(a.tail_start);
     if (b < ts) return BlockTile{b, 0, 1};
     const uint32_t r = b - ts, sp = static_cast<uint32_t>(a.splits);
-    return BlockTile{static_cast<int64_t>(ts + r / sp), static_cast<int>(r % sp), a.splits};
+    return BlockTile{static_cast<int64_t>(__builtin_amdgcn_readfirstlane(ts + r / sp)),
+                     static_cast<int>(__builtin_amdgcn_readfirstlane(r % sp)), a.splits};
 }
 
 // The raw absmax inputs of block b, fetched with the packed bytes; rebuilt later by absmax_val.
@@ -528,14 +538,14 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const int seg = seg_of_tile(a, tile);
     const uint32_t local = static_cast<uint32_t>(tile - a.tile_start[seg]);
     const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
-    const int64_t p0 = static_cast<int64_t>(local / mtl) * BP;
-    const int64_t m0 = static_cast<int64_t>(local % mtl) * BM;
+    const int64_t p0 = uniform64(static_cast<int64_t>(local / mtl) * BP);
+    const int64_t m0 = uniform64(static_cast<int64_t>(local % mtl) * BM);
     const DevWeight w = a.w[seg];  // by value: kept in registers for the whole loop
     const int64_t K = a.K;
     const int64_t steps = K / BR;
     const int64_t per = bt.nsplit > 1 ? a.per_split : steps;
-    const int64_t s0 = split * per;
-    const int64_t s1 = s0 + per < steps ? s0 + per : steps;
+    const int64_t s0 = uniform64(split * per);
+    const int64_t s1 = uniform64(s0 + per < steps ? s0 + per : steps);
 
     if (w.nested)
         for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = w.code2[i];
@@ -803,12 +813,12 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     const int split = bt.split;
     const uint32_t tile = static_cast<uint32_t>(bt.tile);
     const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
-    const int64_t p0 = static_cast<int64_t>(tile / mtl) * BP;
-    const int64_t m0 = static_cast<int64_t>(tile % mtl) * BM;
+    const int64_t p0 = uniform64(static_cast<int64_t>(tile / mtl) * BP);
+    const int64_t m0 = uniform64(static_cast<int64_t>(tile % mtl) * BM);
     const int64_t K = a.K;
     const int64_t per = bt.nsplit > 1 ? a.per_split : a.total_steps;
-    const int64_t s0 = split * per;
-    const int64_t s1 = s0 + per < a.total_steps ? s0 + per : a.total_steps;
+    const int64_t s0 = uniform64(split * per);
+    const int64_t s1 = uniform64(s0 + per < a.total_steps ? s0 + per : a.total_steps);
 
     for (int s = 0; s < a.nseg; ++s) {
         if (a.w[s].nested)
