@@ -98,6 +98,19 @@ __device__ __forceinline__ float16_t mfma32(const u32x4_t &a, const u32x4_t &b, 
     }
 }
 
+// 16x16x32 MFMA: lane l holds row (A) / column (B) l % 16, k = 8 (l / 16) .. + 7; D lane l
+// holds rows 4 (l / 16) .. + 3 of column l % 16.
+template <int DT>
+__device__ __forceinline__ float4_t mfma16(const u32x4_t &a, const u32x4_t &b, const float4_t &c) {
+    if constexpr (DT == NF4_BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf168_t, a),
+                                                      __builtin_bit_cast(bf168_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                     __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+    }
+}
+
 template <int DT>
 __device__ __forceinline__ float to_f32(uint16_t v) {
     if constexpr (DT == NF4_BF16) return __uint_as_float(static_cast<uint32_t>(v) << 16);
@@ -640,6 +653,168 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
                          m0 + wm * (BM / WM), split, bt.nsplit > 1);
 }
 
+// ------------------------------------------------------------------------ decode forward path
+//
+// Y = X W^T for M <= 16 tokens with K a multiple of 128 (decode), bound by the dequant VALU work
+// and HBM.  A workgroup owns 16 weight rows of one segment and its NW waves split the
+// reduction into contiguous ranges of 128-deep super-steps.  In a super-step lane group
+// g = lane / 16 takes k = 32g .. 32g + 31 of its row (16 packed bytes inside one absmax block)
+// and k-substep ks the 8 values 32g + 8ks ..; the activation B fragments use the same k order
+// (64 contiguous bytes of token lane % 16; tokens >= M read as zero through the buffer range).
+// The packed weights run WS super-steps ahead and the activations XS; prefetches past a
+// wave's range are clamped to its last super-step (cached bytes), so the loop has no
+// branches.  The absmax rebuild is branch-free: without double quantization code2 reads
+// {1, 0, ..} and the uint8 code 0, so 1 * absmax + 0 is the fp32 absmax itself.  The waves'
+// 16x16 partial tiles are added in wave order through LDS (deterministic); no split-K.
+constexpr int64_t kDecodeMaxM = 16;
+constexpr int DK = 128;  // decode super-step
+constexpr int kDecodeWavesPerSimd = 6;  // at most 80 VGPRs
+
+template <int DT>
+__device__ __forceinline__ void epilogue16(const GemmArgs &a, const float4_t &acc, int64_t p,
+                                           int64_t p_end, int64_t col_off, int64_t m) {
+    if (m >= a.M || p >= p_end) return;
+    const int64_t col = col_off + p;
+    float v[4] = {acc.x, acc.y, acc.z, acc.w};
+    if (a.bias) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (p + q < p_end) v[q] += to_f32<DT>(a.bias[col + q]);
+    }
+    uint16_t *dst = static_cast<uint16_t *>(a.out) + m * a.ld_out + col;
+    if (p + 4 <= p_end && a.vec_out) {
+        u32x2_t o;
+        o.x = pack2<DT>(v[0], v[1]);
+        o.y = pack2<DT>(v[2], v[3]);
+        *reinterpret_cast<u32x2_t *>(dst) = o;
+    } else {
+        for (int q = 0; q < 4; ++q)
+            if (p + q < p_end) dst[q] = from_f32<DT>(v[q]);
+    }
+}
+
+template <int DT, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerSimd)))
+void decode_kernel(const GemmArgs a) {
+    constexpr int WS = 4, XS = 2;
+    __shared__ float s_code2[256];
+    __shared__ float4_t s_red[NW > 1 ? NW - 1 : 1][64];
+
+    const int64_t tile = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(blockIdx.x));
+    const int seg = seg_of_tile(a, tile);
+    const int64_t p0 = uniform64((tile - a.tile_start[seg]) * 16);
+    const DevWeight w = a.w[seg];
+    const int64_t K = a.K;
+    const int ss = static_cast<int>(K / DK);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int per = (ss + NW - 1) / NW;
+    const int w0 = wave * per < ss ? wave * per : ss;
+    const int w1 = w0 + per < ss ? w0 + per : ss;
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+
+    for (int i = threadIdx.x; i < 256; i += NW * 64)
+        s_code2[i] = w.nested ? w.code2[i] : (i == 0 ? 1.0f : 0.0f);
+    const float abs_off = w.nested ? w.offset : 0.0f;
+    float code_r[16];
+    load_code_sgpr(w.code, code_r);
+
+    const WeightRsrc wr = weight_rsrc(w);
+    const int64_t row = p0 + r;
+    const int wpk = static_cast<int>(row * (K >> 1) + 16 * g);
+    const int wblk = static_cast<int>(row * (K >> wr.bs_shift));
+    const int64_t mrows = a.M < 16 ? a.M : 16;
+    const rsrc_t xr = make_rsrc(a.act, ((mrows - 1) * a.ld_act + a.act_cols) * 2);
+    const int xoff = static_cast<int>((r * a.ld_act + 32 * g) * 2);
+
+    struct WStage {
+        u32x4_t raw;
+        AbsIn abs;
+    };
+    struct XStage {
+        u32x4_t x[4];
+    };
+    const int last = w1 > w0 ? w1 - 1 : w0;
+    auto cl = [&](int v) { return v < last ? v : last; };
+    auto wload = [&](WStage &s, int st) {
+        s.raw = bload16(wr.packed, wpk + st * (DK / 2));
+        s.abs = absmax_bload(wr, wblk + ((st * DK + 32 * g) >> wr.bs_shift));
+    };
+    // lanes of tokens >= M issue no activation loads (their fragments stay zero): at M = 1 the
+    // vector memory unit then spends its address cycles on the weights
+    const bool xlane = r < mrows;
+    auto xload = [&](XStage &s, int st) {
+        if (xlane) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) s.x[ks] = bload16(xr, xoff + st * (DK * 2) + ks * 16);
+        }
+    };
+    // LoRA slab on the last wave, before any prefetch is in flight (its loads are waited for
+    // in full): acc = scale * B[p rows] . T[m rows]^T, rank in 32-deep MFMA chunks, zero-padded
+    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const LoraDev &lo = a.lora[seg];
+    if (lo.has && wave == NW - 1) {
+        for (int k0 = 0; k0 < lo.rank; k0 += 32) {
+            const int lim = lo.rank - (k0 + 8 * g);
+            const u32x4_t fa = (row < w.rows && lim > 0) ? gather8(lo.b + row * lo.rank + k0 + 8 * g, 1, lim)
+                                                         : (u32x4_t){0u, 0u, 0u, 0u};
+            const u32x4_t fb = (r < a.M && lim > 0) ? gather8(lo.t + r * lo.rank + k0 + 8 * g, 1, lim)
+                                                    : (u32x4_t){0u, 0u, 0u, 0u};
+            acc = mfma16<DT>(fa, fb, acc);
+        }
+        acc *= lo.scale;
+    }
+
+    // Loads complete in issue order, so each super-step issues its activation prefetch before
+    // its weight prefetch: waiting for the activations of step s then never waits for weights
+    // younger than step s + WS - 1.
+    WStage ws[WS];
+    XStage xs[XS] = {};
+#pragma unroll
+    for (int b = 0; b < XS; ++b) xload(xs[b], cl(w0 + b));
+#pragma unroll
+    for (int b = 0; b < WS; ++b) wload(ws[b], cl(w0 + b));
+    __syncthreads();  // code2 table
+
+    auto compute = [&](const WStage &s, const XStage &x) {
+        const float sc = __fadd_rn(__fmul_rn(s_code2[s.abs.q], s.abs.s), abs_off);
+        const Nf4Table tb = make_table<DT>(code_r, sc);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint32_t wd = ks == 0 ? s.raw.x : ks == 1 ? s.raw.y : ks == 2 ? s.raw.z : s.raw.w;
+            acc = mfma16<DT>(lookup8(tb, wd), x.x[ks], acc);
+        }
+    };
+    int st = w0;
+    for (; st + WS <= w1; st += WS) {
+#pragma unroll
+        for (int b = 0; b < WS; ++b) {
+            compute(ws[b], xs[b % XS]);
+            __builtin_amdgcn_sched_barrier(0);
+            xload(xs[b % XS], cl(st + b + XS));
+            wload(ws[b], cl(st + b + WS));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < WS - 1; ++b) {
+        if (st + b < w1) {
+            compute(ws[b], xs[b % XS]);
+            xload(xs[b % XS], cl(st + b + XS));
+        }
+    }
+
+    if constexpr (NW > 1) {
+        if (wave > 0) s_red[wave - 1][lane] = acc;
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int v = 0; v < NW - 1; ++v) acc += s_red[v][lane];
+        }
+    }
+    if (wave == 0) epilogue16<DT>(a, acc, p0 + 4 * g, w.rows, a.seg_off[seg], r);
+}
+
 // ------------------------------------------------------------------- small-M forward path
 //
 // Y = X W^T for M <= 32 * MT tokens, MT 1 or 2 (the decode regime), bound by reading the packed
@@ -994,11 +1169,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial,
 // ------------------------------------------------------------------------------ host side
 
 struct Plan {
-    int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves, 2: small-M path
+    int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves, 2: small-M path,
+                   // 4: decode path (M <= 16)
     int bp, bm;
     int splits;    // reduction splits of the tail tiles
     int64_t tiles;
-    int waves;     // small-M path: waves per workgroup
+    int waves;     // small-M and decode paths: waves per workgroup
     int64_t tail_start;  // first split tile (tiles before it run whole)
 
     int64_t blocks() const { return tail_start + (tiles - tail_start) * splits; }
@@ -1124,7 +1300,20 @@ Plan plan_gemv(int64_t m, const nf4_weight *ws, int nw) {
     return Plan{2, 32, 32 * mt, static_cast<int>(splits), tiles, waves, splits > 1 ? 0 : tiles};
 }
 
+// Decode path: waves per 16-row tile, the most (up to 16) that keep the whole launch resident
+// (kDecodeWavesPerSimd waves per SIMD) and give every wave at least three super-steps (fewer
+// make the cross-wave reduction and the prefetch ramp dominate).
+Plan plan_decode(const nf4_weight *ws, int nw) {
+    int64_t tiles = 0;
+    for (int i = 0; i < nw; ++i) tiles += (ws[i].rows + 15) / 16;
+    const int64_t ss = ws[0].cols / DK;
+    int waves = 16;
+    while (waves > 1 && (tiles * waves > 4 * kDecodeWavesPerSimd * kCUs || 3 * waves > ss)) waves /= 2;
+    return Plan{4, 16, 16, 1, tiles, waves, tiles};
+}
+
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
+    if (m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
     if (m <= kGemvMaxM) return plan_gemv(m, ws, nw);
     int64_t big = 0, small = 0;
     for (int i = 0; i < nw; ++i) {
@@ -1148,7 +1337,14 @@ Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
 template <int DT>
 int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
-    if (p.cfg == 2) {
+    if (p.cfg == 4) {
+        const dim3 block(p.waves * 64);
+        if (p.waves == 16) hipLaunchKernelGGL((decode_kernel<DT, 16>), grid, block, 0, st, g);
+        else if (p.waves == 8) hipLaunchKernelGGL((decode_kernel<DT, 8>), grid, block, 0, st, g);
+        else if (p.waves == 4) hipLaunchKernelGGL((decode_kernel<DT, 4>), grid, block, 0, st, g);
+        else if (p.waves == 2) hipLaunchKernelGGL((decode_kernel<DT, 2>), grid, block, 0, st, g);
+        else hipLaunchKernelGGL((decode_kernel<DT, 1>), grid, block, 0, st, g);
+    } else if (p.cfg == 2) {
         const dim3 block(p.waves * 64);
         if (p.bm == 32) {
             if (p.waves == 16) hipLaunchKernelGGL((gemv_kernel<DT, 1, 16>), grid, block, 0, st, g);

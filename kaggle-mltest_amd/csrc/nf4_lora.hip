@@ -76,6 +76,7 @@ struct Jobs {
 // many loads in flight, also when M is a handful of tokens) and add their 16 x 16 partial tiles
 // through LDS in a fixed order.  MFMA A operand = W (rows j), B operand = act (cols m).
 constexpr int kRowdotWaves = 16;
+constexpr int kRowdotUnroll = 8;
 
 template <int DT, bool B_LAYOUT>
 __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jobs, int64_t m,
@@ -96,17 +97,25 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jo
     for (int j0 = 0; j0 < rank; j0 += 16) {
         float4_t acc = {0.f, 0.f, 0.f, 0.f};
         const int j = j0 + col;
-        for (int64_t k0 = kb; k0 < ke; k0 += 32) {
-            const int64_t kk = k0 + kq;
-            const int lim = ke - kk < 8 ? static_cast<int>(ke - kk) : 8;
-            u32x4_t fa = {0u, 0u, 0u, 0u}, fb = {0u, 0u, 0u, 0u};
-            if (lim > 0) {
-                if (j < rank)
-                    fa = B_LAYOUT ? frag8(w + kk * rank + j, rank, lim, false)
-                                  : frag8(w + j * k + kk, 1, lim, (jb.vec & 2) != 0);
-                if (row < m) fb = frag8(act + row * ld + kk, 1, lim, (jb.vec & 1) != 0);
+        // kRowdotUnroll 32-deep slices per group: all their loads are issued before the first
+        // MFMA, so a wave waits for one memory latency per group, not per slice
+        for (int64_t k0 = kb; k0 < ke; k0 += 32 * kRowdotUnroll) {
+            u32x4_t fa[kRowdotUnroll], fb[kRowdotUnroll];
+#pragma unroll
+            for (int u = 0; u < kRowdotUnroll; ++u) {
+                const int64_t kk = k0 + 32 * u + kq;
+                const int lim = ke - kk < 8 ? static_cast<int>(ke - kk) : 8;
+                fa[u] = (u32x4_t){0u, 0u, 0u, 0u};
+                fb[u] = (u32x4_t){0u, 0u, 0u, 0u};
+                if (lim > 0) {
+                    if (j < rank)
+                        fa[u] = B_LAYOUT ? frag8(w + kk * rank + j, rank, lim, false)
+                                         : frag8(w + j * k + kk, 1, lim, (jb.vec & 2) != 0);
+                    if (row < m) fb[u] = frag8(act + row * ld + kk, 1, lim, (jb.vec & 1) != 0);
+                }
             }
-            acc = mfma16<DT>(fa, fb, acc);
+#pragma unroll
+            for (int u = 0; u < kRowdotUnroll; ++u) acc = mfma16<DT>(fa[u], fb[u], acc);
         }
         red[wave][lane] = acc;
         __syncthreads();

@@ -60,6 +60,25 @@ def test_fused_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape,bs,nested", [((136, 384), 64, True), ((40, 1024), 128, True),
+                                             ((72, 256), 64, False)])
+def test_decode_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
+    """The decode path (M <= 16): 16 one-hot activation rows X = I[c0:c0+16] give the weight
+    columns c0 .. c0+15 exactly, for every column block; rows past a 16-row weight tile, plain
+    fp32 absmax and block 128 included."""
+    from solution import kernels
+
+    n, k = shape
+    banner("decode dequant exact", shape, bs, nested, dtype)
+    p, qs = random_weight(n, k, seed=n + 3 * k, dev=cuda, blocksize=bs, nested=nested)
+    ref = oracle_w16(p, qs, "bf16" if dtype == torch.bfloat16 else "f16").view(torch.int16)
+    eye = torch.eye(k, dtype=dtype, device=cuda)
+    for c0 in range(0, k, 16):
+        y = kernels.linear_fwd(eye[c0:c0 + 16], [(p, qs)])
+        assert torch.equal(y.t().contiguous().cpu().view(torch.int16), ref[:, c0:c0 + 16]), c0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("proj", list(QWEN_15B))
 def test_qwen_projection_m2048(cuda, proj, dtype):
     from solution import kernels
