@@ -171,8 +171,15 @@ struct AbsIn {
     uint32_t q;   // uint8 code (nested)
 };
 
+// Branch-free over the weight's format: the kernels' code2 tables hold {1, 0, ..} for a weight
+// without double quantization, whose uint8 code reads 0 (empty resource), so 1 * s + 0 rebuilds
+// the fp32 absmax s exactly (absmax >= 0: no -0 to lose).
+__device__ __forceinline__ float code2_entry(const DevWeight &w, int i) {
+    return w.nested ? w.code2[i] : (i == 0 ? 1.0f : 0.0f);
+}
+
 __device__ __forceinline__ float absmax_val(const DevWeight &w, const AbsIn &in, const float *code2) {
-    return w.nested ? __fadd_rn(__fmul_rn(code2[in.q], in.s), w.offset) : in.s;
+    return __fadd_rn(__fmul_rn(code2[in.q], in.s), w.nested ? w.offset : 0.0f);
 }
 
 // Resources of one weight: packed bytes, uint8 absmax codes (nested) and the fp32 scale array
@@ -560,8 +567,7 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const int64_t s0 = uniform64(split * per);
     const int64_t s1 = uniform64(s0 + per < steps ? s0 + per : steps);
 
-    if (w.nested)
-        for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = w.code2[i];
+    for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = code2_entry(w, i);
     float code_r[16];
     load_code_sgpr(w.code, code_r);
 
@@ -660,12 +666,11 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
 // reduction into contiguous ranges of 128-deep super-steps.  In a super-step lane group
 // g = lane / 16 takes k = 32g .. 32g + 31 of its row (16 packed bytes inside one absmax block)
 // and k-substep ks the 8 values 32g + 8ks ..; the activation B fragments use the same k order
-// (64 contiguous bytes of token lane % 16; tokens >= M read as zero through the buffer range).
+// (64 contiguous bytes of token lane % 16; lanes of tokens >= M load nothing and keep zeros).
 // The packed weights run WS super-steps ahead and the activations XS; prefetches past a
 // wave's range are clamped to its last super-step (cached bytes), so the loop has no
-// branches.  The absmax rebuild is branch-free: without double quantization code2 reads
-// {1, 0, ..} and the uint8 code 0, so 1 * absmax + 0 is the fp32 absmax itself.  The waves'
-// 16x16 partial tiles are added in wave order through LDS (deterministic); no split-K.
+// branches.  The waves' 16x16 partial tiles are added in wave order through LDS
+// (deterministic); no split-K.
 constexpr int64_t kDecodeMaxM = 16;
 constexpr int DK = 128;  // decode super-step
 constexpr int kDecodeWavesPerSimd = 6;  // at most 80 VGPRs
@@ -713,9 +718,7 @@ void decode_kernel(const GemmArgs a) {
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
 
-    for (int i = threadIdx.x; i < 256; i += NW * 64)
-        s_code2[i] = w.nested ? w.code2[i] : (i == 0 ? 1.0f : 0.0f);
-    const float abs_off = w.nested ? w.offset : 0.0f;
+    for (int i = threadIdx.x; i < 256; i += NW * 64) s_code2[i] = code2_entry(w, i);
     float code_r[16];
     load_code_sgpr(w.code, code_r);
 
@@ -777,8 +780,7 @@ void decode_kernel(const GemmArgs a) {
     __syncthreads();  // code2 table
 
     auto compute = [&](const WStage &s, const XStage &x) {
-        const float sc = __fadd_rn(__fmul_rn(s_code2[s.abs.q], s.abs.s), abs_off);
-        const Nf4Table tb = make_table<DT>(code_r, sc);
+        const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, s.abs, s_code2));
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const uint32_t wd = ks == 0 ? s.raw.x : ks == 1 ? s.raw.y : ks == 2 ? s.raw.z : s.raw.w;
@@ -882,7 +884,7 @@ void gemv_kernel(const GemmArgs a) {
     };
     // table loads first: waiting for them (in issue order) then never waits for the prefetch
     float c2 = 0.f;
-    if (w.nested && threadIdx.x < 256) c2 = w.code2[threadIdx.x];
+    if (threadIdx.x < 256) c2 = code2_entry(w, threadIdx.x);
     float code_r[16];
     load_code_sgpr(w.code, code_r);
     const int64_t last = w1 > w0 ? w1 - 1 : w0;
@@ -890,7 +892,7 @@ void gemv_kernel(const GemmArgs a) {
     Stage g[3];
 #pragma unroll
     for (int b = 0; b < 3; ++b) load(g[b], cl(w0 + b));
-    if (w.nested && threadIdx.x < 256) s_code2[threadIdx.x] = c2;
+    if (threadIdx.x < 256) s_code2[threadIdx.x] = c2;
 
     float16_t acc[1][MT];
 #pragma unroll
@@ -995,10 +997,8 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     const int64_t s0 = uniform64(split * per);
     const int64_t s1 = uniform64(s0 + per < a.total_steps ? s0 + per : a.total_steps);
 
-    for (int s = 0; s < a.nseg; ++s) {
-        if (a.w[s].nested)
-            for (int i = threadIdx.x; i < 256; i += NT) s_code2[s][i] = a.w[s].code2[i];
-    }
+    for (int s = 0; s < a.nseg; ++s)
+        for (int i = threadIdx.x; i < 256; i += NT) s_code2[s][i] = code2_entry(a.w[s], i);
 
     const int wave = threadIdx.x >> 6;
     const int wp = wave % WP, wm = wave / WP;

@@ -76,7 +76,6 @@ struct Jobs {
 // many loads in flight, also when M is a handful of tokens) and add their 16 x 16 partial tiles
 // through LDS in a fixed order.  MFMA A operand = W (rows j), B operand = act (cols m).
 constexpr int kRowdotWaves = 16;
-constexpr int kRowdotUnroll = 8;
 
 template <int DT, bool B_LAYOUT>
 __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jobs, int64_t m,
@@ -97,8 +96,10 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jo
     for (int j0 = 0; j0 < rank; j0 += 16) {
         float4_t acc = {0.f, 0.f, 0.f, 0.f};
         const int j = j0 + col;
-        // kRowdotUnroll 32-deep slices per group: all their loads are issued before the first
-        // MFMA, so a wave waits for one memory latency per group, not per slice
+        // U 32-deep slices per group: all their loads are issued before the first MFMA, so a
+        // wave waits for one memory latency per group, not per slice (the strided B-layout
+        // gathers hold 8 scalar loads per fragment: two slices fit the registers)
+        constexpr int kRowdotUnroll = B_LAYOUT ? 2 : 8;
         for (int64_t k0 = kb; k0 < ke; k0 += 32 * kRowdotUnroll) {
             u32x4_t fa[kRowdotUnroll], fb[kRowdotUnroll];
 #pragma unroll
