@@ -63,6 +63,8 @@ def parse():
                     help="skip the Qwen2.5-7B bf16 M=8192 layer (config 4)")
     ap.add_argument("--no-gemv", action="store_true",
                     help="skip the small-M forward sweeps over the 28-layer stacks")
+    ap.add_argument("--no-swiglu", action="store_true",
+                    help="skip the gate|up + SwiGLU epilogue comparison")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times: the "
@@ -145,6 +147,54 @@ def _time_steps(torch, fn, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+# ------------------------------------------------------------- gate|up with SwiGLU epilogue
+
+def swiglu_leg(dtype, dev, reps=20, warmup=3):
+    """The MLP's gate|up step at M=2048 (Qwen2.5-1.5B: I 8960, K 1536) with the SwiGLU step in
+    the GEMM epilogue vs the stacked GEMM writing [M, 2I] followed by the SwiGLU kernel; forward
+    (H) and backward (recompute + dG|dU)."""
+    import torch
+
+    from solution import kernels
+    from solution.quant_state import quantize_4bit
+
+    inter, k = 8960, 1536
+    g = torch.Generator(device=dev)
+    w = []
+    for s in (201, 202):
+        g.manual_seed(s)
+        packed, qs = quantize_4bit(torch.randn(inter, k, generator=g, device=dev) * 0.02)
+        w.append((packed.view(-1), qs))
+    gate, up = w
+    g.manual_seed(203)
+    x = torch.randn(M, k, generator=g, device=dev).to(dtype)
+    dh = (torch.randn(M, inter, generator=g, device=dev) * 1e-2).to(dtype)
+    h = torch.empty(M, inter, dtype=dtype, device=dev)
+    gu = torch.empty(M, 2 * inter, dtype=dtype, device=dev)
+
+    def unfused_fwd():
+        kernels.linear_fwd(x, [gate, up], out=gu)
+        kernels.swiglu_fwd(gu[:, :inter], gu[:, inter:])
+
+    def unfused_bwd():
+        kernels.linear_fwd(x, [gate, up], out=gu)
+        kernels.swiglu_bwd(dh, gu[:, :inter], gu[:, inter:], gu[:, :inter], gu[:, inter:])
+
+    t = {"fused_fwd": lambda: kernels.linear_swiglu_fwd(x, gate, up, out=h),
+         "unfused_fwd": unfused_fwd,
+         "fused_bwd": lambda: kernels.linear_swiglu_bwd(x, gate, up, dh, out=gu),
+         "unfused_bwd": unfused_bwd}
+    res = {n: round(_time_steps(torch, fn, reps, warmup) * 1e3, 2) for n, fn in t.items()}
+    gflop = 2 * M * 2 * inter * k / 1e9
+    return {"mlp_swiglu": {
+        "workload": "Qwen2.5-1.5B gate|up (2 x 8960 x 1536) + SwiGLU, M=2048; fused = SwiGLU in "
+                    "the GEMM epilogue (no [M, 2I] round trip), unfused = stacked GEMM + kernel",
+        "us": res, "gflop": round(gflop, 3),
+        "fused_fwd_tflops": round(gflop / res["fused_fwd"] * 1e3, 1),
+        "speedup_fwd": round(res["unfused_fwd"] / res["fused_fwd"], 3),
+        "speedup_bwd": round(res["unfused_bwd"] / res["fused_bwd"], 3)}}
 
 
 # -------------------------------------------------------------------- varlen stack (config 3)
@@ -469,6 +519,8 @@ def main():
         out["dequant"] = dict(dq, roofline={"bound": "hbm", "achieved": dq["gbps"],
                                             "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                             "frac": dq["frac"], "traffic": None})
+    if not args.no_swiglu:
+        out.update(swiglu_leg(dtype, dev))
     if not args.no_stack:
         out.update(varlen_stack_leg(dtype, dev, gemv=not args.no_gemv))
     if not args.no_7b:

@@ -171,6 +171,22 @@ int nf4_lora_wgrad_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int ran
                          void *workspace, size_t workspace_bytes, void *stream);
 size_t nf4_lora_wgrad_multi_workspace(const nf4_lora_job *jobs, int njobs, int64_t m, int rank);
 
+/* The gate | up pair of an MLP with the SwiGLU step fused into the GEMM epilogue, so the
+ * [M, 2I] gate|up product never reaches memory.  gate_up: two weights of equal shape [I, K]
+ * (gate, then up).  Forward: H[M, I] = silu(X Wg^T) * (X Wu^T), computed in fp32 from the fp32
+ * accumulators and rounded once.  Backward (gate and up recomputed from X): with g, u those
+ * products and sig = 1 / (1 + exp(-g)),
+ *   dGU[:, 0:I]  = dH * u * sig * (1 + g (1 - sig)),   dGU[:, I:2I] = dH * g * sig,
+ * the [M, 2I] gate|up gradient that nf4_linear_dx over the same pair consumes.  No workspace.
+ * Replaces: the gate|up GEMM + gate_up_act_fwd_kernel / gate_up_act_bwd_kernel of
+ *           FusedDecoderLayer (layer.py:266-296, 914-919, 1015-1019) and RecomputedMLP's
+ *           gate, up, _swiglu_fwd / _swiglu_bwd (mlp.py:47-52, 65-70). */
+int nf4_linear_swiglu_fwd(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_up,
+                          void *h, int64_t ldh, int dtype, void *stream);
+int nf4_linear_swiglu_bwd(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_up,
+                          const void *dh, int64_t lddh, void *dgu, int64_t lddgu, int dtype,
+                          void *stream);
+
 /* -------------------------------------------------------------------------- small helpers */
 
 /* out[rows, cols] = silu(gate) * up, and its gradient (the SwiGLU step between the gate/up and

@@ -84,7 +84,9 @@ struct GemmArgs {
     int64_t p_tiles;              // dx: tiles along K
     int64_t total_steps;          // dx: sum of step counts
     int accumulate;               // dx: add into out
-    int vec_out;                  // 8-byte output stores allowed
+    int vec_out;                  // 8-byte output stores allowed (paired: and aux loads)
+    const uint16_t *aux;          // paired SwiGLU backward: dH [M, I]
+    int64_t ld_aux;
 };
 
 template <int DT>
@@ -291,8 +293,17 @@ __device__ __forceinline__ rsrc_t act_rsrc(const GemmArgs &a, int64_t m0) {
 
 // ------------------------------------------------------------------------- MFMA core
 
+// LDS tile row of a wave's weight fragment i: consecutive 32-row fragments from prow0, or for a
+// paired (gate | up) tile with halves of PH rows the first TP / 2 fragments from prow0 in the
+// gate half and the last TP / 2 at the same rows of the up half.
+template <int TP, int PH>
+__device__ __forceinline__ int frag_row(int prow0, int i) {
+    if constexpr (PH == 0) return prow0 + i * 32;
+    else return i < TP / 2 ? prow0 + i * 32 : PH + prow0 + (i - TP / 2) * 32;
+}
+
 // Wave-level MFMA over one 64-deep step: acc[TP][TM] += Wop[p rows] x Act[m rows].
-template <int DT, int TP, int TM>
+template <int DT, int TP, int TM, int PH = 0>
 __device__ __forceinline__ void mma_step(float16_t (&acc)[TP][TM], const uint8_t *sw,
                                          const uint8_t *sa, int prow0, int mrow0) {
     const int lane = threadIdx.x & 63;
@@ -304,7 +315,7 @@ __device__ __forceinline__ void mma_step(float16_t (&acc)[TP][TM], const uint8_t
         u32x4_t fa[TP], fb[TM];
 #pragma unroll
         for (int i = 0; i < TP; ++i)
-            fa[i] = *reinterpret_cast<const u32x4_t *>(sw + swz(prow0 + i * 32 + r, c));
+            fa[i] = *reinterpret_cast<const u32x4_t *>(sw + swz(frag_row<TP, PH>(prow0, i) + r, c));
 #pragma unroll
         for (int j = 0; j < TM; ++j)
             fb[j] = *reinterpret_cast<const u32x4_t *>(sa + swz(mrow0 + j * 32 + r, c));
@@ -318,7 +329,7 @@ __device__ __forceinline__ void mma_step(float16_t (&acc)[TP][TM], const uint8_t
 // mma_step with part ks of the next tile's staging work (`part(ks)`: global-to-LDS copy and
 // dequantization of data already in registers) placed among the MFMAs of k-substep ks, so the
 // VALU and LDS-write work runs while the matrix unit is busy.
-template <int DT, int TP, int TM, class Part>
+template <int DT, int TP, int TM, int PH = 0, class Part>
 __device__ __forceinline__ void mma_step_interleaved(float16_t (&acc)[TP][TM], const uint8_t *sw,
                                                      const uint8_t *sa, int prow0, int mrow0,
                                                      Part &&part) {
@@ -331,7 +342,7 @@ __device__ __forceinline__ void mma_step_interleaved(float16_t (&acc)[TP][TM], c
         u32x4_t fa[TP], fb[TM];
 #pragma unroll
         for (int i = 0; i < TP; ++i)
-            fa[i] = *reinterpret_cast<const u32x4_t *>(sw + swz(prow0 + i * 32 + r, c));
+            fa[i] = *reinterpret_cast<const u32x4_t *>(sw + swz(frag_row<TP, PH>(prow0, i) + r, c));
 #pragma unroll
         for (int j = 0; j < TM; ++j)
             fb[j] = *reinterpret_cast<const u32x4_t *>(sa + swz(mrow0 + j * 32 + r, c));
@@ -539,41 +550,146 @@ __device__ __forceinline__ void mma_step_dx(float16_t (&acc)[TP][TM], const uint
     }
 }
 
+// SwiGLU epilogue of a paired (gate | up) tile: fragments i < TP / 2 hold gate rows j and
+// fragments i + TP / 2 the same up rows, so a lane holds g and u of the same (m, j).
+//   forward:  H[m][j] = silu(g) u                                 (out [M, I])
+//   backward: dG[m][j] = dH u silu'(g), dU[m][j] = dH silu(g)     (out [M, 2I]: dG | dU)
+// with silu'(g) = sig (1 + g (1 - sig)), sig = 1 / (1 + exp(-g)), the standalone SwiGLU
+// kernels' formulas applied to the fp32 accumulators instead of rounded g and u; the reciprocal
+// is the hardware's (1 ulp) instead of a correctly rounded division: the epilogue runs after
+// each tile's main loop, where a dozen-instruction division per element shows.  The dH loads
+// of a lane are all issued before its first use.
+template <int DT, int TP, int TM, bool BWD>
+__device__ __forceinline__ void epilogue_swiglu(const GemmArgs &a, float16_t (&acc)[TP][TM],
+                                                int64_t j_base, int64_t n_inter, int64_t m_base) {
+    const int lane = threadIdx.x & 63;
+    // dH of every (m, 4 j) group of the lane, loaded before any is used (zero outside)
+    u32x2_t dhv[TM][TP / 2][4];
+    if constexpr (BWD) {
+#pragma unroll
+        for (int jm = 0; jm < TM; ++jm) {
+            const int64_t m = m_base + jm * 32 + (lane & 31);
+#pragma unroll
+            for (int i = 0; i < TP / 2; ++i)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int64_t j = j_base + i * 32 + r4 * 8 + (lane >> 5) * 4;
+                    u32x2_t v = {0u, 0u};
+                    if (m < a.M && j < n_inter) {
+                        const uint16_t *src = a.aux + m * a.ld_aux + j;
+                        if (j + 4 <= n_inter && a.vec_out) {
+                            v = *reinterpret_cast<const u32x2_t *>(src);
+                        } else {
+                            uint32_t e[4] = {0u, 0u, 0u, 0u};
+                            for (int q = 0; q < 4; ++q)
+                                if (j + q < n_inter) e[q] = src[q];
+                            v = (u32x2_t){e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+                        }
+                    }
+                    dhv[jm][i][r4] = v;
+                }
+        }
+    }
+#pragma unroll
+    for (int jm = 0; jm < TM; ++jm) {
+        const int64_t m = m_base + jm * 32 + (lane & 31);
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int i = 0; i < TP / 2; ++i) {
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int64_t j = j_base + i * 32 + r4 * 8 + (lane >> 5) * 4;
+                if (j >= n_inter) continue;
+                const bool full = j + 4 <= n_inter && a.vec_out;
+                float dh[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (BWD) {
+                    const u32x2_t v = dhv[jm][i][r4];
+                    dh[0] = to_f32<DT>(v.x & 0xffff);
+                    dh[1] = to_f32<DT>(v.x >> 16);
+                    dh[2] = to_f32<DT>(v.y & 0xffff);
+                    dh[3] = to_f32<DT>(v.y >> 16);
+                }
+                float o0[4], o1[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float g = acc[i][jm][r4 * 4 + q], u = acc[i + TP / 2][jm][r4 * 4 + q];
+                    const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+                    if constexpr (BWD) {
+                        o0[q] = dh[q] * u * sig * (1.0f + g * (1.0f - sig));
+                        o1[q] = dh[q] * g * sig;
+                    } else {
+                        o0[q] = g * sig * u;
+                    }
+                }
+                uint16_t *dst = static_cast<uint16_t *>(a.out) + m * a.ld_out + j;
+#pragma unroll
+                for (int h = 0; h < (BWD ? 2 : 1); ++h) {
+                    const float *v = h == 0 ? o0 : o1;
+                    uint16_t *d = dst + h * n_inter;
+                    if (full) {
+                        u32x2_t o;
+                        o.x = pack2<DT>(v[0], v[1]);
+                        o.y = pack2<DT>(v[2], v[3]);
+                        *reinterpret_cast<u32x2_t *>(d) = o;
+                    } else {
+                        for (int q = 0; q < 4; ++q)
+                            if (j + q < n_inter) d[q] = from_f32<DT>(v[q]);
+                    }
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------- kernels
 
-template <int DT, int BP, int BM, int WP, int WM>
+// EPI 0: Y = X W^T (+ bias, + LoRA), split-K tails allowed.  EPI 1 / 2: paired gate | up
+// tiles (segments 0 and 1, equal shapes) with the SwiGLU forward / backward epilogue: a tile
+// covers BP / 2 rows j of both weights, gate in the first half of its W tile (dequantized by
+// the first half of the waves) and up in the second, no bias, LoRA or split.
+template <int DT, int BP, int BM, int WP, int WM, int EPI = 0>
 __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     constexpr int NT = WP * WM * 64;
     constexpr int TP = BP / WP / 32, TM = BM / WM / 32;
+    constexpr bool PAIR = EPI != 0;
+    constexpr int PH = PAIR ? BP / 2 : 0;
     static_assert(NT == 2 * BP, "forward weight tile mapping needs 2 threads per row");
+    static_assert(!PAIR || TP % 2 == 0, "paired tiles split each wave's fragments in halves");
     __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BP * ROWB];
     __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
-    __shared__ float s_code2[256];
+    __shared__ float s_code2[PAIR ? 2 : 1][256];
 
     // tiles: segments in order, m fastest.  32-bit tile arithmetic: 64-bit divisions are long
     // scalar sequences the whole CU waits on.
     const BlockTile bt = block_tile(a);
     const int split = bt.split;
     const int64_t tile = bt.tile;
-    const int seg = seg_of_tile(a, tile);
+    const int seg = PAIR ? 0 : seg_of_tile(a, tile);
     const uint32_t local = static_cast<uint32_t>(tile - a.tile_start[seg]);
     const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
-    const int64_t p0 = uniform64(static_cast<int64_t>(local / mtl) * BP);
+    const int64_t p0 = uniform64(static_cast<int64_t>(local / mtl) * (PAIR ? PH : BP));
     const int64_t m0 = uniform64(static_cast<int64_t>(local % mtl) * BM);
-    const DevWeight w = a.w[seg];  // by value: kept in registers for the whole loop
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    // the weight this thread dequantizes (paired: the waves of W tile rows >= PH take up)
+    const int wseg = PAIR ? (wave >= BP / 64 ? 1 : 0) : seg;
+    const DevWeight w = a.w[wseg];  // by value: kept in registers for the whole loop
     const int64_t K = a.K;
     const int64_t steps = K / BR;
     const int64_t per = bt.nsplit > 1 ? a.per_split : steps;
     const int64_t s0 = uniform64(split * per);
     const int64_t s1 = uniform64(s0 + per < steps ? s0 + per : steps);
 
-    for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = code2_entry(w, i);
+    for (int i = threadIdx.x; i < 256; i += NT) {
+        s_code2[0][i] = code2_entry(a.w[seg], i);
+        if constexpr (PAIR) s_code2[1][i] = code2_entry(a.w[1], i);
+    }
+    const float *code2 = s_code2[PAIR ? wseg : 0];
     float code_r[16];
     load_code_sgpr(w.code, code_r);
 
-    const int wave = threadIdx.x >> 6;
     const int wp = wave % WP, wm = wave / WP;
     const int lane = threadIdx.x & 63;
+    const int prow0 = wp * ((PAIR ? PH : BP) / WP);  // first W tile row of this wave's fragments
 
     float16_t acc[TP][TM];
 #pragma unroll
@@ -583,7 +699,7 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
 
     // LoRA slab(s): acc = scale * B[p rows] . T[m rows]^T, before the weight product.
     const LoraDev &lo = a.lora[seg];
-    if (lo.has && split == 0) {
+    if (!PAIR && lo.has && split == 0) {
         const int r = lane & 31, kh = (lane >> 5) * 8;
         for (int k0 = 0; k0 < lo.rank; k0 += 16) {
             const int lim = lo.rank - (k0 + kh);
@@ -625,7 +741,7 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const WeightRsrc wr = weight_rsrc(w);
     const rsrc_t ar = act_rsrc<BM>(a, m0);
     const ActAddr aa = act_addr<NT>(a.ld_act);
-    const WAddr wa = fwd_waddr<BP>(wr, p0, K);
+    const WAddr wa = fwd_waddr<BP>(wr, p0 - (wseg == 1 ? PH : 0), K);
     if (s0 < s1) {
         at[0].load(ar, aa, static_cast<int>(s0) * (BR * 2));
         wt[0].load(wr, wa, s0);
@@ -633,7 +749,7 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
         wt[1].load(wr, wa, s0 + 1);
         at[0].store(sA[0]);
         {
-            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, s_code2));
+            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
 #pragma unroll
             for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
         }
@@ -644,19 +760,22 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
             for (int b = 0; b < 2; ++b) {
                 at[b].load(ar, aa, static_cast<int>(st + b + 2) * (BR * 2));
                 wt[b].load(wr, wa, st + b + 2);
-                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, s_code2));
-                mma_step_interleaved<DT, TP, TM>(
-                    acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
+                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
+                mma_step_interleaved<DT, TP, TM, PH>(
+                    acc, sW[b], sA[b], prow0, wm * (BM / WM), [&](int ks) {
                         at[b ^ 1].store_part(sA[b ^ 1], ks);
                         wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
                     });
                 __syncthreads();
             }
         }
-        if (st < s1) mma_step<DT, TP, TM>(acc, sW[0], sA[0], wp * (BP / WP), wm * (BM / WM));
+        if (st < s1) mma_step<DT, TP, TM, PH>(acc, sW[0], sA[0], prow0, wm * (BM / WM));
     }
-    epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), w.rows, a.seg_off[seg],
-                         m0 + wm * (BM / WM), split, bt.nsplit > 1);
+    if constexpr (PAIR)
+        epilogue_swiglu<DT, TP, TM, EPI == 2>(a, acc, p0 + prow0, a.w[0].rows, m0 + wm * (BM / WM));
+    else
+        epilogue<DT, TP, TM>(a, acc, p0 + prow0, w.rows, a.seg_off[seg], m0 + wm * (BM / WM),
+                             split, bt.nsplit > 1);
 }
 
 // ------------------------------------------------------------------------ decode forward path
@@ -1255,13 +1374,13 @@ double plan_cost(int cfg, int64_t tiles, int64_t mt, int64_t tail_start, int spl
     return c;
 }
 
-Plan make_plan(int64_t m, int64_t big, int64_t small, int64_t steps) {
+Plan make_plan(int64_t m, int64_t big, int64_t small, int64_t steps, int max_splits = kMaxSplits) {
     Plan best{};
     double best_cost = 0.0;
     for (int cfg = 0; cfg < 2; ++cfg) {
         const int64_t tiles = cfg == 0 ? big : small;
         const int64_t mt = (m + (cfg == 0 ? 255 : 127)) / (cfg == 0 ? 256 : 128);
-        for (int s = 1; s <= kMaxSplits; ++s) {
+        for (int s = 1; s <= max_splits; ++s) {
             const int64_t per = (steps + s - 1) / s;
             if (s > 1 && (s - 1) * per >= steps) break;  // no empty split
             // the split tail starts at a p-tile boundary (a column range of the output)
@@ -1358,6 +1477,16 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
         hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
     else
         hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2>), grid, dim3(256), 0, st, g);
+    return status_of(hipGetLastError());
+}
+
+template <int DT, int EPI>
+int launch_paired(const GemmArgs &g, const Plan &p, hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(p.blocks()));
+    if (p.cfg == 0)
+        hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4, EPI>), grid, dim3(512), 0, st, g);
+    else
+        hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2, EPI>), grid, dim3(256), 0, st, g);
     return status_of(hipGetLastError());
 }
 
@@ -1536,4 +1665,58 @@ extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_
     if (st != NF4_OK || p.splits <= 1) return st;
     return dtype == NF4_BF16 ? launch_reduce<NF4_BF16>(g, p.splits, s)
                              : launch_reduce<NF4_F16>(g, p.splits, s);
+}
+
+namespace {
+
+// The gate | up pair with the SwiGLU epilogue (forward: out = H [M, I]; backward: aux = dH,
+// out = dG | dU [M, 2I]).  Tiles of the 256x256 or 128x128 forward kernel, chosen by the same
+// cost model over the stacked 2I rows, never split (the epilogue needs whole sums).
+int paired_swiglu(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_up, void *out,
+                  int64_t ldo, const void *aux, int64_t ld_aux, int dtype, bool bwd, void *stream) {
+    if (dtype != NF4_F16 && dtype != NF4_BF16) return NF4_ERR_ARG;
+    if (m < 0 || !out || (m > 0 && !x) || (bwd && m > 0 && !aux)) return NF4_ERR_ARG;
+    GemmArgs g;
+    int st = fill_common(g, x, m, ldx, gate_up, 2);
+    if (st != NF4_OK) return st;
+    const int64_t inter = gate_up[0].rows;
+    if (gate_up[1].rows != inter) return NF4_ERR_ARG;
+    if (ldo < (bwd ? 2 * inter : inter) || (bwd && ld_aux < inter)) return NF4_ERR_ARG;
+    if (m == 0 || inter == 0) return NF4_OK;
+    g.act_cols = g.K;
+    g.out = out;
+    g.ld_out = ldo;
+    g.n_out = bwd ? 2 * inter : inter;
+    g.aux = static_cast<const uint16_t *>(aux);
+    g.ld_aux = ld_aux;
+    g.vec_out = aligned(out, 8) && ldo % 4 == 0 &&
+                (!bwd || (inter % 4 == 0 && aligned(aux, 8) && ld_aux % 4 == 0));
+    const int64_t big = ((inter + 127) / 128) * ((m + 255) / 256);
+    const int64_t small = ((inter + 63) / 64) * ((m + 127) / 128);
+    const Plan p = make_plan(m, big, small, g.K / BR, 1);
+    g.splits = 1;
+    g.per_split = g.K / BR;
+    g.m_tiles = (m + p.bm - 1) / p.bm;
+    g.tile_start[0] = 0;
+    g.tile_start[1] = p.tiles;
+    g.tail_start = p.tiles;
+    g.tail_col0 = g.n_out;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == NF4_BF16)
+        return bwd ? launch_paired<NF4_BF16, 2>(g, p, s) : launch_paired<NF4_BF16, 1>(g, p, s);
+    return bwd ? launch_paired<NF4_F16, 2>(g, p, s) : launch_paired<NF4_F16, 1>(g, p, s);
+}
+
+}  // namespace
+
+extern "C" int nf4_linear_swiglu_fwd(const void *x, int64_t m, int64_t ldx,
+                                     const nf4_weight *gate_up, void *h, int64_t ldh, int dtype,
+                                     void *stream) {
+    return paired_swiglu(x, m, ldx, gate_up, h, ldh, nullptr, 0, dtype, false, stream);
+}
+
+extern "C" int nf4_linear_swiglu_bwd(const void *x, int64_t m, int64_t ldx,
+                                     const nf4_weight *gate_up, const void *dh, int64_t lddh,
+                                     void *dgu, int64_t lddgu, int dtype, void *stream) {
+    return paired_swiglu(x, m, ldx, gate_up, dgu, lddgu, dh, lddh, dtype, true, stream);
 }

@@ -164,6 +164,46 @@ def lora_wgrad(u: torch.Tensor, v: torch.Tensor, scale: float, transpose_out: bo
     return out
 
 
+def _pair(gate, up):
+    if tuple(gate[1].shape) != tuple(up[1].shape):
+        raise ValueError("gate and up weights must have the same shape")
+    return _descs([gate, up])
+
+
+def linear_swiglu_fwd(x: torch.Tensor, gate, up, out: torch.Tensor | None = None) -> torch.Tensor:
+    """H[M, I] = silu(x @ Wg^T) * (x @ Wu^T), the SwiGLU step in the gate|up GEMM's epilogue.
+    `gate`, `up`: (packed, quant_state) pairs of equal shape [I, K]."""
+    _check_device(x)
+    m = x.shape[0]
+    inter = int(gate[1].shape[0])
+    if out is None:
+        out = torch.empty((m, inter), dtype=x.dtype, device=x.device)
+    arr = _pair(gate, up)
+    st = load().nf4_linear_swiglu_fwd(x.data_ptr() if m else None, m, x.stride(0), arr,
+                                      out.data_ptr(), out.stride(0), _code(x.dtype), stream_of(x))
+    check(st, "nf4_linear_swiglu_fwd")
+    return out
+
+
+def linear_swiglu_bwd(x: torch.Tensor, gate, up, d_hidden: torch.Tensor,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """dGU[M, 2I] (dgate | dup) from d_hidden [M, I] and gate/up recomputed from x inside the
+    GEMM; the input of linear_dx over the stacked (gate, up) pair."""
+    _check_device(x, d_hidden)
+    m = x.shape[0]
+    inter = int(gate[1].shape[0])
+    if tuple(d_hidden.shape) != (m, inter) or d_hidden.stride(1) != 1:
+        raise ValueError("d_hidden must be a row-contiguous [M, I] tensor")
+    if out is None:
+        out = torch.empty((m, 2 * inter), dtype=x.dtype, device=x.device)
+    arr = _pair(gate, up)
+    st = load().nf4_linear_swiglu_bwd(x.data_ptr() if m else None, m, x.stride(0), arr,
+                                      d_hidden.data_ptr(), d_hidden.stride(0), out.data_ptr(),
+                                      out.stride(0), _code(x.dtype), stream_of(x))
+    check(st, "nf4_linear_swiglu_bwd")
+    return out
+
+
 def swiglu_fwd(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up for two [M, I] views with equal row stride (e.g. halves of gate|up)."""
     _check_device(gate, up)

@@ -2,9 +2,12 @@
 on the HIP kernels.  Mirror of /root/reference/solution/mlp.py (`RecomputedMLP`, 42-74, same
 apply() signature; `patch_qwen2_mlp_recompute`, 123-157).
 
-gate and up run as ONE stacked dequant-GEMM launch ([M, 2I] output), the SwiGLU step reads its
-two halves in place, and the input gradient dgate W_gate + dup W_up is ONE transposed
-dequant-GEMM over the stacked pair, summed in fp32 (the reference adds two fp16 products).
+gate and up run as ONE dequant-GEMM launch over the pair with the SwiGLU step in its epilogue
+(nf4_linear_swiglu_fwd: the [M, 2I] gate|up product never reaches memory); the backward
+recomputes them the same way with the SwiGLU gradient in the epilogue (nf4_linear_swiglu_bwd),
+and the input gradient dgate W_gate + dup W_up is ONE transposed dequant-GEMM over the stacked
+pair, summed in fp32 (the reference adds two fp16 products).  Below FUSED_MIN_TOKENS rows
+(decode) the unfused sequence runs: the stacked small-M GEMM, then the SwiGLU kernels.
 The reference's recompute budget (mlp.py:92-120) is a 15 GB-GPU memory policy and is not
 mirrored: this MLP always recomputes.
 """
@@ -17,6 +20,11 @@ from . import kernels
 from .quant_state import nf4_state_ok
 
 
+# Token count from which the gate|up GEMM carries the SwiGLU epilogue (its tiles are the large
+# forward tiles; the decode-size GEMM paths keep the separate SwiGLU step).
+FUSED_MIN_TOKENS = 65
+
+
 class RecomputedMLP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, gate_w, gate_qs, up_w, up_qs, down_w, down_qs):
@@ -26,9 +34,12 @@ class RecomputedMLP(torch.autograd.Function):
             x2 = x2.contiguous()
         gate_w, up_w, down_w = gate_w.reshape(-1), up_w.reshape(-1), down_w.reshape(-1)
         inter = int(gate_qs.shape[0])
-        gu = kernels.linear_fwd(x2, [(gate_w, gate_qs), (up_w, up_qs)])
-        hidden = kernels.swiglu_fwd(gu[:, :inter], gu[:, inter:])
-        del gu
+        if x2.shape[0] >= FUSED_MIN_TOKENS:
+            hidden = kernels.linear_swiglu_fwd(x2, (gate_w, gate_qs), (up_w, up_qs))
+        else:
+            gu = kernels.linear_fwd(x2, [(gate_w, gate_qs), (up_w, up_qs)])
+            hidden = kernels.swiglu_fwd(gu[:, :inter], gu[:, inter:])
+            del gu
         out = kernels.linear_fwd(hidden, [(down_w, down_qs)])
         ctx.save_for_backward(x2, gate_w, up_w, down_w)
         ctx.qs, ctx.shape = (gate_qs, up_qs, down_qs), shape
@@ -43,9 +54,13 @@ class RecomputedMLP(torch.autograd.Function):
         if grad.stride(0) % 8 or grad.data_ptr() % 16:
             grad = grad.contiguous()
         d_hidden = kernels.linear_dx(grad, [(down_w, down_qs)])
-        gu = kernels.linear_fwd(x2, [(gate_w, gate_qs), (up_w, up_qs)])
-        # the gradient of gate|up overwrites gate|up (each element is read, then written)
-        kernels.swiglu_bwd(d_hidden, gu[:, :inter], gu[:, inter:], gu[:, :inter], gu[:, inter:])
+        if x2.shape[0] >= FUSED_MIN_TOKENS:
+            gu = kernels.linear_swiglu_bwd(x2, (gate_w, gate_qs), (up_w, up_qs), d_hidden)
+        else:
+            gu = kernels.linear_fwd(x2, [(gate_w, gate_qs), (up_w, up_qs)])
+            # the gradient of gate|up overwrites gate|up (each element is read, then written)
+            kernels.swiglu_bwd(d_hidden, gu[:, :inter], gu[:, inter:], gu[:, :inter],
+                               gu[:, inter:])
         del d_hidden
         dx = kernels.linear_dx(gu, [(gate_w, gate_qs), (up_w, up_qs)])
         return dx.view(ctx.shape), None, None, None, None, None, None

@@ -258,3 +258,28 @@ def test_lora_multi_matches_single(cuda, dtype):
         # the multi launch reduces over the widest job's chunking: equal within fp32 rounding
         torch.testing.assert_close(gb[i], ref_b, rtol=1e-5, atol=1e-7)
         torch.testing.assert_close(ga[i], ref_a, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,inter,k", [(2048, 8960, 1536), (300, 200, 320), (129, 1000, 256)])
+def test_swiglu_epilogue(cuda, m, inter, k, dtype):
+    """gate | up with the SwiGLU step in the GEMM epilogue: H = silu(g) u and the gradients
+    dG = dH u silu'(g), dU = dH silu(g) against the fp32 oracle (g, u = X W^T on the bit-exact
+    weights), at the Qwen2.5-1.5B MLP shape and ragged ones (I not a multiple of the tile)."""
+    from solution import kernels
+
+    banner("swiglu epilogue", m, inter, k, dtype)
+    dt = "bf16" if dtype == torch.bfloat16 else "f16"
+    gate = random_weight(inter, k, seed=inter + 1, dev=cuda)
+    up = random_weight(inter, k, seed=inter + 2, dev=cuda)
+    wg, wu = oracle_w16(*gate, dt), oracle_w16(*up, dt)
+    x = _x(m, k, 61, cuda, dtype)
+    dh = _x(m, inter, 62, cuda, dtype, std=1e-2)
+    g, u = o.linear_fwd(x, wg), o.linear_fwd(x, wu)
+    sig = 1.0 / (1.0 + torch.exp(-g))
+    h = kernels.linear_swiglu_fwd(x, gate, up)
+    assert_rel(h, g * sig * u, what="H")
+    dgu = kernels.linear_swiglu_bwd(x, gate, up, dh)
+    d = dh.float().cpu()
+    assert_rel(dgu[:, :inter], d * u * sig * (1.0 + g * (1.0 - sig)), what="dG")
+    assert_rel(dgu[:, inter:], d * g * sig, what="dU")

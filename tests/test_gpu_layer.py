@@ -79,18 +79,20 @@ def test_qkv_projection_with_lora_grads(cuda, dtype):
         assert_rel(got, ref.grad, mean_rel=3e-3 if dtype == torch.bfloat16 else 1e-3, what=name)
 
 
-def test_recomputed_mlp_matches_fp32(cuda):
-    """The reference's MLP test shapes (gate/up 1024x512, down 512x1024, x [1, 200, 512])."""
+@pytest.mark.parametrize("tokens", [200, 8])
+def test_recomputed_mlp_matches_fp32(cuda, tokens):
+    """The reference's MLP test shapes (gate/up 1024x512, down 512x1024, x [1, 200, 512]): the
+    fused SwiGLU-epilogue path; and 8 tokens, below FUSED_MIN_TOKENS (separate SwiGLU step)."""
     from solution.mlp import RecomputedMLP
 
-    banner("RecomputedMLP")
+    banner("RecomputedMLP", tokens)
     gate = random_weight(1024, 512, seed=1, dev=cuda, std=0.05)
     up = random_weight(1024, 512, seed=2, dev=cuda, std=0.05)
     down = random_weight(512, 1024, seed=3, dev=cuda, std=0.05)
     wg, wu, wd = (oracle_w16(p, q).float() for p, q in (gate, up, down))
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(1, 200, 512, generator=g).half().to(cuda).requires_grad_()
-    grad = torch.randn(1, 200, 512, generator=g).half().to(cuda)
+    x = torch.randn(1, tokens, 512, generator=g).half().to(cuda).requires_grad_()
+    grad = torch.randn(1, tokens, 512, generator=g).half().to(cuda)
     out = RecomputedMLP.apply(x, gate[0], gate[1], up[0], up[1], down[0], down[1])
     out.backward(grad)
     xr = x.detach().float().cpu().requires_grad_()
