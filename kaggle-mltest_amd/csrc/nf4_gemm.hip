@@ -1343,8 +1343,9 @@ int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const n
 
 // Tile and split choice by a cost model whose constants were measured on MI355X (fp16, M = 2048,
 // every Qwen2.5-1.5B projection, each plan timed): one 64-deep step of a 256x256 tile takes
-// ~2.6 us with one workgroup per CU; a 128x128 step ~1.35 us alone on a CU and ~1.6 us with two
-// workgroups per CU.  Workgroups run in rounds of 256 (256x256) or 512 (128x128).  Split-K adds
+// ~2.45 us with one workgroup per CU; a 128x128 step ~1.15 us alone on a CU and ~1.4 us with two
+// workgroups per CU.  Workgroups run in rounds of 256 (256x256) or 512 (128x128); a last
+// 128x128 round of at most 256 workgroups runs one per CU at the single-workgroup speed.  Split-K adds
 // the fp32 partial round trip (written by the GEMM, read back by the reduction) at ~5 TB/s plus
 // ~12 us of reduction launch and tail.  The larger tile needs 4x fewer dequant instructions per
 // MFMA, which the step times already contain.
@@ -1360,10 +1361,12 @@ double plan_cost(int cfg, int64_t tiles, int64_t mt, int64_t tail_start, int spl
     const int64_t bp = cfg == 0 ? 256 : 128;
     const int64_t full = splits > 1 ? tail_start : tiles;
     const int64_t tail_blocks = splits > 1 ? (tiles - tail_start) * splits : 0;
-    const double t_step = cfg == 0 ? 2.6 : (full + tail_blocks <= kCUs ? 1.35 : 1.6);
+    const double t_step = cfg == 0 ? 2.45 : (full + tail_blocks <= kCUs ? 1.15 : 1.4);
     const int64_t per = (steps + splits - 1) / splits;
     const int64_t rounds = (full + slots - 1) / slots;
     double c = double(rounds) * double(steps) * t_step + 1.0;
+    if (cfg == 1 && full > kCUs && full % slots != 0 && full % slots <= kCUs && tail_blocks == 0)
+        c -= double(steps) * (t_step - 1.15);  // the last round alone on its CUs
     const int64_t free_slots = rounds * slots - full;
     if (tail_blocks > free_slots)
         c += double((tail_blocks - free_slots + slots - 1) / slots) * double(per) * t_step;
