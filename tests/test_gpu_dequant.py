@@ -142,3 +142,20 @@ def test_batch_bit_exact(cuda, dt):
     for (p, qs), out in zip(odd, views):
         assert torch.equal(_bits(out).reshape(-1), _oracle(p, qs, dt).reshape(-1))
     assert _bits(buf[:1]).item() == 0
+
+
+@pytest.mark.parametrize("nested", [True, False])
+def test_checkpoint_loads_into_kernels(cuda, tmp_path, nested):
+    """A weight saved in bitsandbytes' serialized layout and loaded straight onto the GPU feeds
+    the kernels unchanged: dequant bit-exact against the oracle on the loaded state, and the
+    same bytes as the weight before saving."""
+    from solution.checkpoint import load_safetensors, save_safetensors
+    from solution.nf4 import dequantize_nf4
+
+    banner("checkpoint -> kernels", nested)
+    packed, qs = random_weight(200, 512, seed=77, dev=cuda, nested=nested)
+    save_safetensors(tmp_path / "w.safetensors", {"layer.q_proj.": (packed, qs)})
+    p2, q2 = load_safetensors(tmp_path / "w.safetensors", cuda)["layer.q_proj."]
+    w = dequantize_nf4(p2, q2, torch.float16)
+    assert torch.equal(w.cpu().view(torch.int16), oracle_w16(p2, q2).view(torch.int16))
+    assert torch.equal(w, dequantize_nf4(packed, qs, torch.float16))
