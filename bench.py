@@ -65,6 +65,8 @@ def parse():
                     help="skip the small-M forward sweeps over the 28-layer stacks")
     ap.add_argument("--no-swiglu", action="store_true",
                     help="skip the gate|up + SwiGLU epilogue comparison")
+    ap.add_argument("--no-norm-rope", action="store_true",
+                    help="skip the RMSNorm / RoPE neighbours of the projection")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times: the "
@@ -195,6 +197,52 @@ def swiglu_leg(dtype, dev, reps=20, warmup=3):
         "fused_fwd_tflops": round(gflop / res["fused_fwd"] * 1e3, 1),
         "speedup_fwd": round(res["unfused_fwd"] / res["fused_fwd"], 3),
         "speedup_bwd": round(res["unfused_bwd"] / res["fused_bwd"], 3)}}
+
+
+# ------------------------------------------------- the projection's neighbours (norm, RoPE)
+
+def norm_rope_leg(dtype, dev, reps=20):
+    """RMSNorm (+ residual, + LoRA dropout inputs) and RoPE forward and backward at M=2048 on
+    the Qwen2.5-1.5B shapes (hidden 1536, 12 query heads, 2 key/value heads of 128): GB/s of
+    algorithmic bytes against the 8 TB/s HBM peak, each kernel replayed 20 times in a HIP
+    graph (these launches are a few microseconds each)."""
+    import torch
+
+    from solution import kernels
+
+    h, nh, nkv, hd = 1536, 12, 2, 128
+    g = torch.Generator(device=dev).manual_seed(301)
+    r = lambda *s: torch.randn(*s, generator=g, device=dev).to(dtype)  # noqa: E731
+    x, d, dy, dq, dv, dres = (r(M, h) for _ in range(6))
+    w = torch.rand(h, generator=g, device=dev) + 0.5
+    keep = lambda: (torch.rand(M, h, generator=g, device=dev) > 0.1).to(torch.uint8)  # noqa: E731
+    kq, kv = keep(), keep()
+    _, rstd = kernels.add_rmsnorm(x, w, 1e-6, d=d)
+    qkv = r(M, (nh + 2 * nkv) * hd)
+    ang = torch.rand(M, hd // 2, generator=g, device=dev)
+    cos, sin = torch.cat([ang.cos()] * 2, 1), torch.cat([ang.sin()] * 2, 1)
+    gq, gk, gv = (r(M, nh, hd) for _ in range(3))
+    e = 2  # bytes per element
+    legs = {
+        "rmsnorm_fwd": (lambda: kernels.add_rmsnorm(x, w, 1e-6, d=d, keep_q=kq, keep_v=kv,
+                                                    scale_q=1.1, scale_v=1.1),
+                        M * h * (2 * e + 2 + 3 * e) + M * 4 + h * 4),
+        "rmsnorm_bwd": (lambda: kernels.rmsnorm_bwd(x, w, rstd, dy=dy, d=d, dres=dres, dq=dq, dv=dv,
+                                                    keep_q=kq, keep_v=kv),
+                        M * h * (6 * e + 2 + e) + M * 4 + h * 4),
+        "rope_fwd": (lambda: kernels.qkv_rope(qkv, cos, sin, nh, nkv, hd),
+                     M * ((nh + 2 * nkv) * hd * e + 2 * hd * 4 + 3 * nh * hd * e + 2 * nkv * hd * e)),
+        "rope_bwd": (lambda: kernels.qkv_rope_bwd(gq, gk, gv, cos, sin, nkv),
+                     M * (3 * nh * hd * e + 2 * hd * 4 + (nh + 2 * nkv) * hd * e)),
+    }
+    out = {}
+    for name, (fn, nbytes) in legs.items():
+        ms = _time_graph(torch, lambda fn=fn: [fn() for _ in range(reps)], 3) / reps
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "gbps": round(gbps, 1),
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "bytes": nbytes}
+    return {"norm_rope": dict(out, workload="RMSNorm + RoPE fwd/bwd around the q|k|v projection, "
+                                           "Qwen2.5-1.5B shapes, M=2048, HIP graph replay")}
 
 
 # -------------------------------------------------------------------- varlen stack (config 3)
@@ -521,6 +569,8 @@ def main():
                                             "frac": dq["frac"], "traffic": None})
     if not args.no_swiglu:
         out.update(swiglu_leg(dtype, dev))
+    if not args.no_norm_rope:
+        out.update(norm_rope_leg(dtype, dev))
     if not args.no_stack:
         out.update(varlen_stack_leg(dtype, dev, gemv=not args.no_gemv))
     if not args.no_7b:

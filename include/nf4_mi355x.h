@@ -187,6 +187,47 @@ int nf4_linear_swiglu_bwd(const void *x, int64_t m, int64_t ldx, const nf4_weigh
                           const void *dh, int64_t lddh, void *dgu, int64_t lddgu, int dtype,
                           void *stream);
 
+/* ------------------------------------------- the projection's neighbours: RMSNorm, RoPE */
+
+/* One row per token (contiguous [rows, cols] tensors, cols a multiple of 8, at most 8192):
+ * h = x (+ d), rstd[r] = 1 / sqrt(mean(h^2) + eps), y = w * (h * rstd) in fp32 rounded once to
+ * dtype; w is fp32 [cols].  With keep masks (uint8 [rows, cols], 1 = kept, both or neither) also
+ * LoRA's dropout inputs oq = y * keep_q * scale_q, ov = y * keep_v * scale_v.  d may be NULL.
+ * Replaces: add_rmsnorm_fwd_kernel (/root/reference/solution/layer.py:92-132; its masks are
+ *           packed 8 per byte, here one byte per element). */
+int nf4_add_rmsnorm(const void *x, const void *d, const float *w, void *y, float *rstd,
+                    const uint8_t *keep_q, const uint8_t *keep_v, float scale_q, float scale_v,
+                    void *oq, void *ov, int64_t rows, int64_t cols, float eps, int dtype,
+                    void *stream);
+
+/* The gradient of the above: g = dy (+ dq * keep_q * scale_q + dv * keep_v * scale_v),
+ * h = x (+ d) recomputed, h^ = h * rstd, dx = rstd * (g w - h^ * mean(g w h^)) (+ dres).
+ * dy, dq/dv (together with the masks), d and dres may be NULL.
+ * Replaces: rmsnorm_bwd_lora_kernel (/root/reference/solution/layer.py:135-164). */
+int nf4_rmsnorm_bwd(const void *dy, const void *dq, const void *dv, const uint8_t *keep_q,
+                    const uint8_t *keep_v, float scale_q, float scale_v, const void *x,
+                    const void *d, const float *w, const float *rstd, const void *dres, void *dx,
+                    int64_t rows, int64_t cols, int dtype, void *stream);
+
+/* Rotary embedding of the finished q|k|v projection (qkv [tokens, ld_qkv], columns n_heads q
+ * heads, n_kv k heads, n_kv v heads of head_dim each; the LoRA terms are already in it, added by
+ * nf4_linear_fwd's epilogue): per pair i < head_dim/2, lo' = lo cos[i] - hi sin[i],
+ * hi' = hi cos[half + i] + lo sin[half + i] on q and k in fp32 (cos, sin fp32 [tokens, head_dim]),
+ * q, k, v written as [tokens, n_heads, head_dim] (k, v expanded to every query head of their
+ * group), and the unexpanded k, v to k_cache / v_cache [tokens, n_kv, head_dim] when given.
+ * Replaces: qkv_lora_rope_kernel (/root/reference/solution/layer.py:167-218) minus its LoRA
+ *           add (layer.py:190-193, 208-211), which moved into the GEMM. */
+int nf4_qkv_rope(const void *qkv, int64_t ld_qkv, const float *cos_t, const float *sin_t,
+                 void *q, void *k, void *v, void *k_cache, void *v_cache, int64_t tokens,
+                 int n_heads, int n_kv, int head_dim, int dtype, void *stream);
+
+/* The gradient of the above into dqkv [tokens, ld_dqkv] (q|k|v columns): the transposed
+ * rotation of dq and of dk summed over each group's expanded heads; dv summed the same way.
+ * Replaces: qkv_rope_bwd_kernel (/root/reference/solution/layer.py:221-263). */
+int nf4_qkv_rope_bwd(const void *dq, const void *dk, const void *dv, const float *cos_t,
+                     const float *sin_t, void *dqkv, int64_t ld_dqkv, int64_t tokens, int n_heads,
+                     int n_kv, int head_dim, int dtype, void *stream);
+
 /* -------------------------------------------------------------------------- small helpers */
 
 /* out[rows, cols] = silu(gate) * up, and its gradient (the SwiGLU step between the gate/up and

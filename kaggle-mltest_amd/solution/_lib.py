@@ -93,6 +93,16 @@ _SIGNATURES = {
     "nf4_swiglu_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
                                c_void_p, c_int64, c_int64, c_int, c_void_p]),
     "nf4_bias_grad": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p]),
+    "nf4_add_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_float, c_float, c_void_p, c_void_p, c_int64, c_int64,
+                                c_float, c_int, c_void_p]),
+    "nf4_rmsnorm_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_float,
+                                c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_int64, c_int64, c_int, c_void_p]),
+    "nf4_qkv_rope": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                             c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p]),
+    "nf4_qkv_rope_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                 c_int64, c_int64, c_int, c_int, c_int, c_int, c_void_p]),
 }
 
 EXPORTS = tuple(_SIGNATURES)

@@ -239,6 +239,92 @@ def bias_grad(dy: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _rows(t, cols):
+    if t is not None and (t.dim() != 2 or t.shape[1] != cols or not t.is_contiguous()):
+        raise ValueError("norm operands are contiguous [rows, cols] tensors")
+
+
+def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, d: torch.Tensor | None = None,
+                keep_q: torch.Tensor | None = None, keep_v: torch.Tensor | None = None,
+                scale_q: float = 1.0, scale_v: float = 1.0):
+    """(y, rstd[, oq, ov]): RMSNorm of x (+ d) with fp32 weight w, y in x's dtype; with uint8
+    keep masks also LoRA's dropout inputs y * keep * scale."""
+    _check_device(x, d, w, keep_q, keep_v)
+    rows, cols = x.shape
+    for t in (d, keep_q, keep_v):
+        _rows(t, cols)
+    _rows(x, cols)
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+    w = w.to(torch.float32).contiguous()
+    oq = ov = None
+    if keep_q is not None:
+        oq, ov = torch.empty_like(x), torch.empty_like(x)
+    st = load().nf4_add_rmsnorm(_p(x), _p(d), _p(w), _p(y), _p(rstd), _p(keep_q), _p(keep_v),
+                                float(scale_q), float(scale_v), _p(oq), _p(ov), rows, cols,
+                                float(eps), _code(x.dtype), stream_of(x))
+    check(st, "nf4_add_rmsnorm")
+    return (y, rstd) if keep_q is None else (y, rstd, oq, ov)
+
+
+def rmsnorm_bwd(x: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor, dy=None, d=None, dres=None,
+                dq=None, dv=None, keep_q=None, keep_v=None, scale_q: float = 1.0,
+                scale_v: float = 1.0) -> torch.Tensor:
+    """dX of add_rmsnorm from the output's gradient dy and LoRA's dropout branches dq, dv, plus
+    the residual gradient dres."""
+    _check_device(x, w, rstd, dy, d, dres, dq, dv, keep_q, keep_v)
+    rows, cols = x.shape
+    for t in (x, dy, d, dres, dq, dv, keep_q, keep_v):
+        _rows(t, cols)
+    dx = torch.empty_like(x)
+    w = w.to(torch.float32).contiguous()
+    st = load().nf4_rmsnorm_bwd(_p(dy), _p(dq), _p(dv), _p(keep_q), _p(keep_v), float(scale_q),
+                                float(scale_v), _p(x), _p(d), _p(w), _p(rstd), _p(dres), _p(dx),
+                                rows, cols, _code(x.dtype), stream_of(x))
+    check(st, "nf4_rmsnorm_bwd")
+    return dx
+
+
+def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_heads: int, n_kv: int,
+             head_dim: int, caches: bool = True):
+    """(q, k, v[, k_cache, v_cache]) from the finished q|k|v projection [tokens, ...]: rotary
+    embedding on q and k, k and v expanded to [tokens, n_heads, head_dim]."""
+    _check_device(qkv, cos, sin)
+    tokens = qkv.shape[0]
+    if qkv.stride(1) != 1:
+        raise ValueError("qkv rows must be contiguous")
+    cos, sin = cos.to(torch.float32).contiguous(), sin.to(torch.float32).contiguous()
+    e = lambda h: torch.empty(tokens, h, head_dim, dtype=qkv.dtype, device=qkv.device)  # noqa: E731
+    q, k, v = e(n_heads), e(n_heads), e(n_heads)
+    kc, vc = (e(n_kv), e(n_kv)) if caches else (None, None)
+    st = load().nf4_qkv_rope(_p(qkv), qkv.stride(0), _p(cos), _p(sin), _p(q), _p(k), _p(v), _p(kc),
+                             _p(vc), tokens, n_heads, n_kv, head_dim, _code(qkv.dtype),
+                             stream_of(qkv))
+    check(st, "nf4_qkv_rope")
+    return (q, k, v, kc, vc) if caches else (q, k, v)
+
+
+def qkv_rope_bwd(dq: torch.Tensor, dk: torch.Tensor, dv: torch.Tensor, cos: torch.Tensor,
+                 sin: torch.Tensor, n_kv: int) -> torch.Tensor:
+    """d(q|k|v) [tokens, (n_heads + 2 n_kv) head_dim] from the gradients of qkv_rope's q, k, v
+    ([tokens, n_heads, head_dim] each)."""
+    _check_device(dq, dk, dv, cos, sin)
+    tokens, n_heads, head_dim = dq.shape
+    for t in (dq, dk, dv):
+        if tuple(t.shape) != (tokens, n_heads, head_dim) or not t.is_contiguous():
+            raise ValueError("dq, dk, dv are contiguous [tokens, n_heads, head_dim] tensors")
+    cos, sin = cos.to(torch.float32).contiguous(), sin.to(torch.float32).contiguous()
+    out = torch.empty(tokens, (n_heads + 2 * n_kv) * head_dim, dtype=dq.dtype, device=dq.device)
+    st = load().nf4_qkv_rope_bwd(_p(dq), _p(dk), _p(dv), _p(cos), _p(sin), _p(out), out.stride(0),
+                                 tokens, n_heads, n_kv, head_dim, _code(dq.dtype), stream_of(dq))
+    check(st, "nf4_qkv_rope_bwd")
+    return out
+
+
 def make_lora(seg: int, rank: int, scale: float, t=None, b=None, a=None, da=None) -> NF4Lora:
     return NF4Lora(seg=seg, rank=rank, scale=float(scale),
                    t=t.data_ptr() if t is not None else None,

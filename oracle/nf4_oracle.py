@@ -325,6 +325,90 @@ def mlp_fwd(x, wg, wu, wd):
     return (silu(g) * u) @ _t(wd).t()
 
 
+# --------------------------------------------------- the projection's neighbours (fp32)
+
+def add_rmsnorm(x, w, eps, d=None, keep_q=None, keep_v=None, scale_q=1.0, scale_v=1.0):
+    """fp32 ``h = x (+ d)``, ``rstd = 1/sqrt(mean(h^2) + eps)``, ``y = w * (h * rstd)`` and
+    LoRA's dropout inputs ``y * keep * scale`` (layer.py:92-132).  Returns (y, rstd, oq, ov)."""
+    h = _t(x)
+    if d is not None:
+        h = h + _t(d)
+    rstd = 1.0 / (h.pow(2).mean(-1, keepdim=True) + float(eps)).sqrt()
+    y = _t(w) * (h * rstd)
+    oq = ov = None
+    if keep_q is not None:
+        oq = y * _t(keep_q) * float(scale_q)
+        ov = y * _t(keep_v) * float(scale_v)
+    return y, rstd.squeeze(-1), oq, ov
+
+
+def rmsnorm_bwd(x, w, rstd, dy=None, d=None, dres=None, dq=None, dv=None, keep_q=None,
+                keep_v=None, scale_q=1.0, scale_v=1.0):
+    """fp32 gradient of add_rmsnorm (layer.py:135-164): ``g = dy + dq*keep_q*s_q +
+    dv*keep_v*s_v``, ``h^ = (x + d) * rstd``, ``dx = rstd (g w - h^ mean(g w h^)) + dres``."""
+    h = _t(x)
+    if d is not None:
+        h = h + _t(d)
+    g = _zeros_like(h)
+    if dy is not None:
+        g = g + _t(dy)
+    if dq is not None:
+        g = g + _t(dq) * _t(keep_q) * float(scale_q) + _t(dv) * _t(keep_v) * float(scale_v)
+    r = _t(rstd).reshape(-1, 1)
+    hh = h * r
+    gw = g * _t(w)
+    dx = r * (gw - hh * (gw * hh).mean(-1, keepdim=True))
+    if dres is not None:
+        dx = dx + _t(dres)
+    return dx
+
+
+def _zeros_like(t):
+    import torch
+
+    return torch.zeros_like(t)
+
+
+def _rotate(lo, hi, cos, sin, half):
+    return (lo * cos[:, None, :half] - hi * sin[:, None, :half],
+            hi * cos[:, None, half:] + lo * sin[:, None, half:])
+
+
+def qkv_rope(qkv, cos, sin, n_heads, n_kv, head_dim):
+    """fp32 rotary embedding of the finished q|k|v projection (layer.py:167-218 without its
+    LoRA add): q, k rotated, k and v expanded to every query head.  Returns (q, k, v, kc, vc)
+    with q, k, v [tokens, n_heads, head_dim] and kc, vc [tokens, n_kv, head_dim]."""
+    import torch
+
+    qkv, cos, sin = _t(qkv), _t(cos), _t(sin)
+    t, half, groups = qkv.shape[0], head_dim // 2, n_heads // n_kv
+    q = qkv[:, :n_heads * head_dim].reshape(t, n_heads, head_dim)
+    k = qkv[:, n_heads * head_dim:(n_heads + n_kv) * head_dim].reshape(t, n_kv, head_dim)
+    v = qkv[:, (n_heads + n_kv) * head_dim:(n_heads + 2 * n_kv) * head_dim].reshape(t, n_kv, head_dim)
+    qr = torch.cat(_rotate(q[..., :half], q[..., half:], cos, sin, half), -1)
+    kr = torch.cat(_rotate(k[..., :half], k[..., half:], cos, sin, half), -1)
+    return (qr, kr.repeat_interleave(groups, 1), v.repeat_interleave(groups, 1), kr, v)
+
+
+def qkv_rope_bwd(dq, dk, dv, cos, sin, n_kv):
+    """fp32 gradient of qkv_rope into the [tokens, q|k|v] layout (layer.py:221-263): the
+    transposed rotation; the expanded copies' gradients summed per key/value head."""
+    import torch
+
+    dq, dk, dv, cos, sin = _t(dq), _t(dk), _t(dv), _t(cos), _t(sin)
+    t, n_heads, head_dim = dq.shape
+    half, groups = head_dim // 2, n_heads // n_kv
+
+    def back(g):
+        lo, hi = g[..., :half], g[..., half:]
+        return torch.cat((lo * cos[:, None, :half] + hi * sin[:, None, half:],
+                          hi * cos[:, None, half:] - lo * sin[:, None, :half]), -1)
+
+    gk = dk.reshape(t, n_kv, groups, head_dim).sum(2)
+    gv = dv.reshape(t, n_kv, groups, head_dim).sum(2)
+    return torch.cat((back(dq).reshape(t, -1), back(gk).reshape(t, -1), gv.reshape(t, -1)), 1)
+
+
 def rel_errors(out, ref) -> tuple[float, float]:
     """(max |out-ref| / max |ref|, mean |out-ref| / mean |ref|): the reference's ``_rel``
     (layer.py:1253-1254) and its mean counterpart."""

@@ -1,5 +1,6 @@
 """Pins the CPU oracle against what mathematics and library routines fix (no GPU)."""
 
+import math
 import numpy as np
 import pytest
 import torch
@@ -185,3 +186,87 @@ def test_rel_errors_definition():
     out = torch.tensor([1.0, -2.0, 4.4])
     mx, mean = o.rel_errors(out, ref)
     assert abs(mx - 0.1) < 1e-6 and abs(mean - (0.4 / 3) / (7 / 3)) < 1e-6
+
+
+# ------------------------------------------------------------ norm and RoPE restatements
+
+def _norm_inputs(rows=5, cols=24, seed=0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    keep = lambda: (torch.rand(rows, cols, generator=g) > 0.3).float()  # noqa: E731
+    return r(rows, cols), r(rows, cols) * 0.5, r(cols).abs() + 0.5, keep(), keep()
+
+
+def test_add_rmsnorm_matches_row_loop():
+    """The vectorised norm against an explicit per-row, per-element fp64 loop."""
+    x, d, w, kq, kv = _norm_inputs()
+    y, rstd, oq, ov = o.add_rmsnorm(x, w, 1e-6, d=d, keep_q=kq, keep_v=kv, scale_q=1.25, scale_v=0.5)
+    for r in range(x.shape[0]):
+        h = [float(x[r, c]) + float(d[r, c]) for c in range(x.shape[1])]
+        rs = 1.0 / math.sqrt(sum(v * v for v in h) / len(h) + 1e-6)
+        assert abs(float(rstd[r]) - rs) <= 1e-6 * rs
+        for c in range(x.shape[1]):
+            yy = float(w[c]) * h[c] * rs
+            assert abs(float(y[r, c]) - yy) <= 1e-5 * (1 + abs(yy))
+            assert abs(float(oq[r, c]) - yy * float(kq[r, c]) * 1.25) <= 1e-5 * (1 + abs(yy))
+            assert abs(float(ov[r, c]) - yy * float(kv[r, c]) * 0.5) <= 1e-5 * (1 + abs(yy))
+
+
+def test_rmsnorm_bwd_matches_autograd():
+    """The hand-written norm gradient (output, both dropout branches, residual) against torch
+    autograd of the forward restatement."""
+    import torch
+
+    x, d, w, kq, kv = _norm_inputs(seed=1)
+    g = torch.Generator().manual_seed(2)
+    gy, gq, gv, gres = (torch.randn(x.shape, generator=g) for _ in range(4))
+    xa, da = x.clone().requires_grad_(), d.clone().requires_grad_()
+    y, rstd, oq, ov = o.add_rmsnorm(xa, w, 1e-6, d=da, keep_q=kq, keep_v=kv, scale_q=2.0, scale_v=3.0)
+    ((y * gy).sum() + (oq * gq).sum() + (ov * gv).sum()).backward()
+    dx = o.rmsnorm_bwd(x, w, rstd.detach(), dy=gy, d=d, dres=gres, dq=gq, dv=gv, keep_q=kq,
+                       keep_v=kv, scale_q=2.0, scale_v=3.0)
+    torch.testing.assert_close(dx, xa.grad + gres, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(da.grad, xa.grad)  # x and d enter as one sum
+
+
+def _rope_inputs(tokens=3, n_heads=6, n_kv=2, head_dim=8, seed=3):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(tokens, (n_heads + 2 * n_kv) * head_dim, generator=g)
+    ang = torch.rand(tokens, head_dim // 2, generator=g) * 6.0
+    cos = torch.cat([ang.cos(), ang.cos()], 1)
+    sin = torch.cat([ang.sin(), ang.sin()], 1)
+    return qkv, cos, sin
+
+
+def test_qkv_rope_identity_norms_and_expansion():
+    """cos = 1, sin = 0 is the identity; a rotation keeps every pair's norm; k and v copies of
+    one group are identical and equal the caches."""
+    import torch
+
+    qkv, cos, sin = _rope_inputs()
+    nh, nkv, hd = 6, 2, 8
+    q, k, v, kc, vc = o.qkv_rope(qkv, torch.ones_like(cos), torch.zeros_like(sin), nh, nkv, hd)
+    assert torch.equal(q.reshape(3, -1), qkv[:, :nh * hd])
+    q, k, v, kc, vc = o.qkv_rope(qkv, cos, sin, nh, nkv, hd)
+    qin = qkv[:, :nh * hd].reshape(3, nh, hd)
+    pair = lambda t: t[..., :hd // 2] ** 2 + t[..., hd // 2:] ** 2  # noqa: E731
+    torch.testing.assert_close(pair(q), pair(qin))
+    for h in range(nh):
+        assert torch.equal(k[:, h], kc[:, h // 3]) and torch.equal(v[:, h], vc[:, h // 3])
+    assert torch.equal(vc.reshape(3, -1), qkv[:, (nh + nkv) * hd:])
+
+
+def test_qkv_rope_bwd_matches_autograd():
+    import torch
+
+    qkv, cos, sin = _rope_inputs(seed=4)
+    g = torch.Generator().manual_seed(5)
+    gq, gk, gv = (torch.randn(3, 6, 8, generator=g) for _ in range(3))
+    qa = qkv.clone().requires_grad_()
+    q, k, v, _, _ = o.qkv_rope(qa, cos, sin, 6, 2, 8)
+    ((q * gq).sum() + (k * gk).sum() + (v * gv).sum()).backward()
+    torch.testing.assert_close(o.qkv_rope_bwd(gq, gk, gv, cos, sin, 2), qa.grad)
