@@ -1434,9 +1434,18 @@ Plan plan_decode(const nf4_weight *ws, int nw) {
     return Plan{4, 16, 16, 1, tiles, waves, tiles};
 }
 
+// Forward path by token count: the decode kernel up to 16 tokens (K a multiple of 128), the
+// small-M kernel up to 32, and from 33 to 64 the small-M kernel only for long reductions over
+// few rows (sum of rows < K); the tiled GEMMs otherwise (measured at M = 64 on the Qwen2.5-1.5B
+// and -7B projections: q|k|v, o and gate|up 4-30 % faster tiled with split-K, the 1.5B down
+// projection 25 % faster on the small-M kernel).
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
     if (m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
-    if (m <= kGemvMaxM) return plan_gemv(m, ws, nw);
+    if (m <= kGemvMaxM) {
+        int64_t n = 0;
+        for (int i = 0; i < nw; ++i) n += ws[i].rows;
+        if (m <= 32 || n < ws[0].cols) return plan_gemv(m, ws, nw);
+    }
     int64_t big = 0, small = 0;
     for (int i = 0; i < nw; ++i) {
         big += (ws[i].rows + 255) / 256;
