@@ -398,13 +398,24 @@ def dequant_leg(dtype, dev, reps=5):
     batch_ms = _time_graph(torch, run_batched, reps)
     group_ms = _time_graph(torch, run_grouped, reps)
     gbps = total_bytes / (batch_ms * 1e-3) / 1e9
+    # the box's own ceilings for this traffic mix: torch's fill (write only) and copy on 2 GiB
+    big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    big2 = torch.empty_like(big)
+    fill_ms = _time_steps(torch, lambda: big.fill_(1), 5, 2)
+    copy_ms = _time_steps(torch, lambda: big2.copy_(big), 5, 2)
+    del big, big2
     return {"gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
             "bytes_per_pass": total_bytes, "us_per_pass": round(batch_ms * 1e3, 1),
             "launches_per_pass": len(batched), "working_set": "28-layer Qwen2.5-1.5B stack",
             "timing": "one nf4_dequant_batch launch per layer (7 weights), HIP graph replay",
             "gbps_grouped_launches": round(total_bytes / (group_ms * 1e-3) / 1e9, 1),
             "grouped": "4 nf4_dequant_multi launches per layer (q|k|v, o, gate|up, down) as the "
-                       "reference's _dequant groups them"}
+                       "reference's _dequant groups them",
+            "box_write_gbps": round((2 << 30) / (fill_ms * 1e-3) / 1e9, 1),
+            "box_copy_gbps": round(2 * (2 << 30) / (copy_ms * 1e-3) / 1e9, 1),
+            "box_note": "torch fill_ (write only) and copy_ (read + write) of 2 GiB on the same "
+                        "box: the dequant moves 0.52 B read + 2 B written per element, so the "
+                        "write rate bounds it"}
 
 
 # ---------------------------------------------------------------------------- CPU baseline
