@@ -125,6 +125,33 @@ int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy,
                   void *workspace, size_t workspace_bytes, void *stream);
 size_t nf4_linear_dx_workspace(int64_t m, const nf4_weight *ws, int nw, int dtype);
 
+/* The same two GEMMs with the tiling pinned instead of chosen by the library's cost model:
+ * tile NF4_TILE_256 (256x256 tiles, 8 waves), NF4_TILE_128 (128x128, 4 waves) or
+ * NF4_TILE_128_KSPLIT2 (128x128, two groups of 4 waves splitting each tile's reduction), with
+ * every tile's reduction further split `splits` ways across workgroups (1 = none; 2..16, no
+ * split may be empty, else NF4_ERR_ARG).  NF4_TILE_AUTO (or any negative tile) is the plain
+ * entry point.  A pinned tiling never takes the small-M kernels.  A workspace of
+ * splits * M * (output columns) * 4 bytes always suffices.  For callers that autotune or that
+ * need one fixed summation order across token counts, and for tests of every tiling.
+ * Replaces: the same reference GEMMs as nf4_linear_fwd / nf4_linear_dx (the reference leaves
+ *           the tiling to cuBLAS). */
+#define NF4_TILE_AUTO (-1)
+#define NF4_TILE_256 0
+#define NF4_TILE_128 1
+#define NF4_TILE_128_KSPLIT2 3
+int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx,
+                         const nf4_weight *ws, int nw, const void *bias,
+                         const nf4_lora *loras, int nlora,
+                         void *y, int64_t ldy, int dtype,
+                         void *workspace, size_t workspace_bytes, void *stream,
+                         int tile, int splits);
+int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy,
+                        const nf4_weight *ws, int nw,
+                        const nf4_lora *loras, int nlora,
+                        void *dx, int64_t lddx, int accumulate, int dtype,
+                        void *workspace, size_t workspace_bytes, void *stream,
+                        int tile, int splits);
+
 /* ---------------------------------------------------------------------- LoRA side GEMMs */
 
 /* t[M, rank] = xd[M, K] @ A[rank, K]^T  (LoRA down-projection; layer.py:875, 877). */
@@ -186,6 +213,12 @@ int nf4_linear_swiglu_fwd(const void *x, int64_t m, int64_t ldx, const nf4_weigh
 int nf4_linear_swiglu_bwd(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_up,
                           const void *dh, int64_t lddh, void *dgu, int64_t lddgu, int dtype,
                           void *stream);
+/* Either of the two with the tiling pinned (NF4_TILE_*, never split; out = H or dGU, dh
+ * ignored forward), for autotuning callers and tests of every tiling.
+ * Replaces: the same reference code as the two above. */
+int nf4_linear_swiglu_tiled(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_up,
+                            void *out, int64_t ldo, const void *dh, int64_t lddh, int dtype,
+                            void *stream, int backward, int tile);
 
 /* ------------------------------------------- the projection's neighbours: RMSNorm, RoPE */
 

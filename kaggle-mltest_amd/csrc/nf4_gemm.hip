@@ -233,7 +233,8 @@ struct ActAddr {
 template <int NT>
 __device__ __forceinline__ ActAddr act_addr(int64_t ld) {
     ActAddr r;
-    r.base = static_cast<int>(((threadIdx.x >> 3) * ld + (threadIdx.x & 7) * 8) * 2);
+    const int t = threadIdx.x % NT;
+    r.base = static_cast<int>(((t >> 3) * ld + (t & 7) * 8) * 2);
     r.rstep = static_cast<int>((NT / 8) * ld * 2);
     return r;
 }
@@ -255,7 +256,7 @@ struct ActTile {
 
     // Zero the elements at columns >= valid of the step (a segment's partial last step).
     __device__ __forceinline__ void mask(int valid) {
-        const int k = valid - static_cast<int>(threadIdx.x & 7) * 8;  // valid elements of my chunks
+        const int k = valid - static_cast<int>(threadIdx.x % NT & 7) * 8;  // valid elements of my chunks
         uint32_t mk[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d)
@@ -268,7 +269,7 @@ struct ActTile {
     __device__ __forceinline__ void store(uint8_t *s) const {
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
-            const int idx = i * NT + threadIdx.x;
+            const int idx = i * NT + threadIdx.x % NT;
             *reinterpret_cast<u32x4_t *>(s + swz(idx >> 3, idx & 7)) = r[i];
         }
     }
@@ -278,7 +279,7 @@ struct ActTile {
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
             if (i % 4 != part) continue;
-            const int idx = i * NT + threadIdx.x;
+            const int idx = i * NT + threadIdx.x % NT;
             *reinterpret_cast<u32x4_t *>(s + swz(idx >> 3, idx & 7)) = r[i];
         }
     }
@@ -368,14 +369,16 @@ __device__ __forceinline__ u32x4_t gather8(const uint16_t *src, int64_t stride, 
 }
 
 // Epilogue: lane holds C[p .. p+3][m] for each (i, j, r4).  Writes either fp32 partials
-// (a split tail tile) or final values (+bias, +existing for accumulate) in DT.
-template <int DT, int TP, int TM>
+// (a split tail tile) or final values (+bias, +existing for accumulate) in DT.  With KG k-groups
+// in the workgroup, group g writes the fragments j with j % KG == g (see group_sum).
+template <int DT, int TP, int TM, int KG = 1>
 __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP][TM],
                                          int64_t p_base, int64_t p_end, int64_t col_off,
-                                         int64_t m_base, int split, bool to_partial) {
+                                         int64_t m_base, int split, bool to_partial, int g = 0) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
+        if (KG > 1 && j % KG != g) continue;  // another k-group's fragments
         const int64_t m = m_base + j * 32 + (lane & 31);
         if (m >= a.M) continue;
 #pragma unroll
@@ -442,9 +445,10 @@ struct WAddr {
 
 template <int BP>
 __device__ __forceinline__ WAddr fwd_waddr(const WeightRsrc &r, int64_t p0, int64_t K) {
-    const int64_t row = p0 + (threadIdx.x >> 1);
+    const int t = threadIdx.x % (2 * BP);
+    const int64_t row = p0 + (t >> 1);
     WAddr a;
-    a.packed = static_cast<int>(row * (K >> 1) + (threadIdx.x & 1) * 16);
+    a.packed = static_cast<int>(row * (K >> 1) + (t & 1) * 16);
     a.block = static_cast<int>(row * (K >> r.bs_shift));
     return a;
 }
@@ -463,7 +467,8 @@ struct FwdWeight {
     // Dword `part` of the 16 packed bytes (8 elements) through the register table of this
     // thread's row (make_table with the row's absmax).
     __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, int part) const {
-        const int row = threadIdx.x >> 1, h = (threadIdx.x & 1) * 4;
+        const int t = threadIdx.x % (2 * BP);
+        const int row = t >> 1, h = (t & 1) * 4;
         const uint32_t wd = part == 0 ? raw.x : part == 1 ? raw.y : part == 2 ? raw.z : raw.w;
         *reinterpret_cast<u32x4_t *>(s + swz(row, h + part)) = lookup8(tb, wd);
     }
@@ -481,7 +486,8 @@ __device__ __forceinline__ int swz_t(int n, int c) {
 template <int BP>
 __device__ __forceinline__ WAddr dx_waddr(const WeightRsrc &r, int64_t p0, int64_t K) {
     constexpr int KQ = BP / 32;
-    const int64_t n = threadIdx.x / KQ, k = p0 + (threadIdx.x % KQ) * 32;
+    const int t = threadIdx.x % (2 * BP);
+    const int64_t n = t / KQ, k = p0 + (t % KQ) * 32;
     WAddr a;
     a.packed = static_cast<int>((n * K + k) >> 1);
     a.block = static_cast<int>(n * (K >> r.bs_shift) + (k >> r.bs_shift));
@@ -502,7 +508,8 @@ struct DxWeight {
     }
 
     __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, int part) const {
-        const int n = threadIdx.x / KQ, c = (threadIdx.x % KQ) * 4 + part;
+        const int t = threadIdx.x % (2 * BP);
+        const int n = t / KQ, c = (t % KQ) * 4 + part;
         const uint32_t wd = part == 0 ? raw.x : part == 1 ? raw.y : part == 2 ? raw.z : raw.w;
         *reinterpret_cast<u32x4_t *>(s + swz_t<BP>(n, c)) = lookup8(tb, wd);
     }
@@ -559,15 +566,17 @@ __device__ __forceinline__ void mma_step_dx(float16_t (&acc)[TP][TM], const uint
 // is the hardware's (1 ulp) instead of a correctly rounded division: the epilogue runs after
 // each tile's main loop, where a dozen-instruction division per element shows.  The dH loads
 // of a lane are all issued before its first use.
-template <int DT, int TP, int TM, bool BWD>
+template <int DT, int TP, int TM, bool BWD, int KG = 1>
 __device__ __forceinline__ void epilogue_swiglu(const GemmArgs &a, float16_t (&acc)[TP][TM],
-                                                int64_t j_base, int64_t n_inter, int64_t m_base) {
+                                                int64_t j_base, int64_t n_inter, int64_t m_base,
+                                                int g = 0) {
     const int lane = threadIdx.x & 63;
     // dH of every (m, 4 j) group of the lane, loaded before any is used (zero outside)
     u32x2_t dhv[TM][TP / 2][4];
     if constexpr (BWD) {
 #pragma unroll
         for (int jm = 0; jm < TM; ++jm) {
+            if (KG > 1 && jm % KG != g) continue;
             const int64_t m = m_base + jm * 32 + (lane & 31);
 #pragma unroll
             for (int i = 0; i < TP / 2; ++i)
@@ -592,6 +601,7 @@ __device__ __forceinline__ void epilogue_swiglu(const GemmArgs &a, float16_t (&a
     }
 #pragma unroll
     for (int jm = 0; jm < TM; ++jm) {
+        if (KG > 1 && jm % KG != g) continue;
         const int64_t m = m_base + jm * 32 + (lane & 31);
         if (m >= a.M) continue;
 #pragma unroll
@@ -643,20 +653,63 @@ __device__ __forceinline__ void epilogue_swiglu(const GemmArgs &a, float16_t (&a
 
 // ------------------------------------------------------------------------------- kernels
 
+// k-groups: a workgroup of KG groups of WP x WM waves; group g takes the steps s0 + g,
+// s0 + g + KG, .. of the workgroup's reduction range through LDS stages of its own, with every
+// group running the same number of steps (a group past the range runs its last step on zero
+// activations), so that all waves meet at the same barriers.  Afterwards the groups add their
+// accumulators through LDS: group g finishes the fragments j with j % KG == g and receives the
+// other groups' values for those (one 16-byte slot per lane, 1 KB per wave instruction).  For
+// KG = 2 the sum of the two groups is the same in either order.
+template <int TP, int TM, int KG, int NT>
+__device__ __forceinline__ void group_sum(float16_t (&acc)[TP][TM], uint8_t *lds, int g) {
+    static_assert(KG == 2 && TM % 2 == 0, "two k-groups over an even number of m fragments");
+    const int gt = threadIdx.x % NT;  // thread inside its group
+    constexpr int ngt = NT;
+    float4_t *slot = reinterpret_cast<float4_t *>(lds);
+    __syncthreads();  // every group's last MFMAs have read the staging tiles
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        if (j % KG == g) continue;
+#pragma unroll
+        for (int i = 0; i < TP; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                slot[((j * TP + i) * 4 + q) * ngt + gt] =
+                    (float4_t){acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                               acc[i][j][4 * q + 3]};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        if (j % KG != g) continue;
+#pragma unroll
+        for (int i = 0; i < TP; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4_t v = slot[((j * TP + i) * 4 + q) * ngt + gt];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
+            }
+    }
+}
+
 // EPI 0: Y = X W^T (+ bias, + LoRA), split-K tails allowed.  EPI 1 / 2: paired gate | up
 // tiles (segments 0 and 1, equal shapes) with the SwiGLU forward / backward epilogue: a tile
 // covers BP / 2 rows j of both weights, gate in the first half of its W tile (dequantized by
-// the first half of the waves) and up in the second, no bias, LoRA or split.
-template <int DT, int BP, int BM, int WP, int WM, int EPI = 0>
-__global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
-    constexpr int NT = WP * WM * 64;
+// the first half of the waves) and up in the second, no bias, LoRA or split.  KG k-groups
+// (group_sum above) split each tile's reduction inside the workgroup.
+template <int DT, int BP, int BM, int WP, int WM, int EPI = 0, int KG = 1>
+__global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) {
+    constexpr int NT = WP * WM * 64;  // threads of one k-group
     constexpr int TP = BP / WP / 32, TM = BM / WM / 32;
     constexpr bool PAIR = EPI != 0;
     constexpr int PH = PAIR ? BP / 2 : 0;
     static_assert(NT == 2 * BP, "forward weight tile mapping needs 2 threads per row");
     static_assert(!PAIR || TP % 2 == 0, "paired tiles split each wave's fragments in halves");
-    __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BP * ROWB];
-    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
+    constexpr int NS = 2;  // LDS stages per k-group
+    static_assert(KG == 1 || BP * BM * 4 <= KG * NS * (BP + BM) * ROWB,
+                  "the k-group sums fit in the staging tiles");
+    __shared__ __attribute__((aligned(1024))) uint8_t sT[KG][NS][(BP + BM) * ROWB];
     __shared__ float s_code2[PAIR ? 2 : 1][256];
 
     // tiles: segments in order, m fastest.  32-bit tile arithmetic: 64-bit divisions are long
@@ -669,7 +722,9 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
     const int64_t p0 = uniform64(static_cast<int64_t>(local / mtl) * (PAIR ? PH : BP));
     const int64_t m0 = uniform64(static_cast<int64_t>(local % mtl) * BM);
-    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int wave_all = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int g = KG > 1 ? wave_all / (WP * WM) : 0;           // k-group
+    const int wave = KG > 1 ? wave_all % (WP * WM) : wave_all;  // wave inside the group
     // the weight this thread dequantizes (paired: the waves of W tile rows >= PH take up)
     const int wseg = PAIR ? (wave >= BP / 64 ? 1 : 0) : seg;
     const DevWeight w = a.w[wseg];  // by value: kept in registers for the whole loop
@@ -678,8 +733,10 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     const int64_t per = bt.nsplit > 1 ? a.per_split : steps;
     const int64_t s0 = uniform64(split * per);
     const int64_t s1 = uniform64(s0 + per < steps ? s0 + per : steps);
+    // this group's steps: s0 + g + KG v for v < nv (the same nv in every group)
+    const int64_t nv = (s1 - s0 + KG - 1) / KG;
 
-    for (int i = threadIdx.x; i < 256; i += NT) {
+    for (int i = threadIdx.x; i < 256; i += KG * NT) {
         s_code2[0][i] = code2_entry(a.w[seg], i);
         if constexpr (PAIR) s_code2[1][i] = code2_entry(a.w[1], i);
     }
@@ -699,7 +756,7 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
 
     // LoRA slab(s): acc = scale * B[p rows] . T[m rows]^T, before the weight product.
     const LoraDev &lo = a.lora[seg];
-    if (!PAIR && lo.has && split == 0) {
+    if (!PAIR && lo.has && split == 0 && g == 0) {
         const int r = lane & 31, kh = (lane >> 5) * 8;
         for (int k0 = 0; k0 < lo.rank; k0 += 16) {
             const int lim = lo.rank - (k0 + kh);
@@ -727,26 +784,33 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
             for (int j = 0; j < TM; ++j) acc[i][j] *= lo.scale;
     }
 
-    // Two register stages (steps st+1 and st+2 in flight) and two LDS stages (st and st+1).
-    // Step st computes from LDS stage (st - s0) & 1 while the other LDS stage receives step
-    // st+1 from register stage (st + 1 - s0) & 1, a quarter per MFMA k-substep; the register
-    // stage of st has been consumed, so it takes the global loads of st+2.  The loop body has
-    // no branches: prefetches past the range are issued anyway (in bounds of the operands or
-    // zero from the buffer range check, never consumed), so the compiler's wait counts only
-    // wait for the loads a store needs, never for the prefetch just issued.  An odd last step
-    // runs after the loop.
+    // Two register stages (steps v+1 and v+2 in flight) and two LDS stages (v and v+1), in the
+    // group's step numbering v.  Step v computes from LDS stage v & 1 while the other LDS stage
+    // receives step v+1 from register stage (v + 1) & 1, a quarter per MFMA k-substep; the
+    // register stage of v has been consumed, so it takes the global loads of v+2.  The loop
+    // body has no branches: prefetches past the range are issued anyway (in bounds of the
+    // operands or zero from the buffer range check, never consumed), so the compiler's wait
+    // counts only wait for the loads a store needs, never for the prefetch just issued.  An odd
+    // last step runs after the loop.  A group's step past the workgroup's range (KG > 1 only)
+    // reads its activations from an empty resource: zeros, so it adds nothing.
     FwdWeight<DT, BP> wt[2] = {};
     ActTile<BM, NT> at[2] = {};
     __syncthreads();  // tables
     const WeightRsrc wr = weight_rsrc(w);
     const rsrc_t ar = act_rsrc<BM>(a, m0);
+    const rsrc_t ar0 = make_rsrc(a.act, 0);
     const ActAddr aa = act_addr<NT>(a.ld_act);
     const WAddr wa = fwd_waddr<BP>(wr, p0 - (wseg == 1 ? PH : 0), K);
-    if (s0 < s1) {
-        at[0].load(ar, aa, static_cast<int>(s0) * (BR * 2));
-        wt[0].load(wr, wa, s0);
-        at[1].load(ar, aa, static_cast<int>(s0 + 1) * (BR * 2));
-        wt[1].load(wr, wa, s0 + 1);
+    auto stage = [&](int b, int64_t v) {
+        const int64_t st = s0 + g + KG * v;
+        at[b].load(KG > 1 && st >= s1 ? ar0 : ar, aa, static_cast<int>(st) * (BR * 2));
+        wt[b].load(wr, wa, st);
+    };
+    uint8_t *sW[2] = {sT[g][0], sT[g][1]};
+    uint8_t *sA[2] = {sT[g][0] + BP * ROWB, sT[g][1] + BP * ROWB};
+    if (nv > 0) {
+        stage(0, 0);
+        stage(1, 1);
         at[0].store(sA[0]);
         {
             const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
@@ -754,12 +818,11 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
             for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
         }
         __syncthreads();
-        int64_t st = s0;
-        for (; st + 1 < s1; st += 2) {
+        int64_t v = 0;
+        for (; v + 1 < nv; v += 2) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                at[b].load(ar, aa, static_cast<int>(st + b + 2) * (BR * 2));
-                wt[b].load(wr, wa, st + b + 2);
+                stage(b, v + b + 2);
                 const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
                 mma_step_interleaved<DT, TP, TM, PH>(
                     acc, sW[b], sA[b], prow0, wm * (BM / WM), [&](int ks) {
@@ -769,13 +832,15 @@ __global__ __launch_bounds__(WP *WM * 64) void fwd_kernel(const GemmArgs a) {
                 __syncthreads();
             }
         }
-        if (st < s1) mma_step<DT, TP, TM, PH>(acc, sW[0], sA[0], prow0, wm * (BM / WM));
+        if (v < nv) mma_step<DT, TP, TM, PH>(acc, sW[0], sA[0], prow0, wm * (BM / WM));
     }
+    if constexpr (KG > 1) group_sum<TP, TM, KG, NT>(acc, &sT[0][0][0], g);
     if constexpr (PAIR)
-        epilogue_swiglu<DT, TP, TM, EPI == 2>(a, acc, p0 + prow0, a.w[0].rows, m0 + wm * (BM / WM));
+        epilogue_swiglu<DT, TP, TM, EPI == 2, KG>(a, acc, p0 + prow0, a.w[0].rows,
+                                                  m0 + wm * (BM / WM), g);
     else
-        epilogue<DT, TP, TM>(a, acc, p0 + prow0, w.rows, a.seg_off[seg], m0 + wm * (BM / WM),
-                             split, bt.nsplit > 1);
+        epilogue<DT, TP, TM, KG>(a, acc, p0 + prow0, w.rows, a.seg_off[seg], m0 + wm * (BM / WM),
+                                 split, bt.nsplit > 1, g);
 }
 
 // ------------------------------------------------------------------------ decode forward path
@@ -1096,13 +1161,15 @@ void gemv_kernel(const GemmArgs a) {
     }
 }
 
-template <int DT, int BP, int BM, int WP, int WM>
-__global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
-    constexpr int NT = WP * WM * 64;
+template <int DT, int BP, int BM, int WP, int WM, int KG = 1>
+__global__ __launch_bounds__(KG *WP *WM * 64) void dx_kernel(const GemmArgs a) {
+    constexpr int NT = WP * WM * 64;  // threads of one k-group
     constexpr int TP = BP / WP / 32, TM = BM / WM / 32;
     static_assert(NT == 2 * BP, "dX weight tile mapping needs 2 threads per k column group");
-    __shared__ __attribute__((aligned(1024))) uint8_t sW[2][BP * ROWB];
-    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BM * ROWB];
+    constexpr int NS = 2;  // LDS stages per k-group
+    static_assert(KG == 1 || BP * BM * 4 <= KG * NS * (BP + BM) * ROWB,
+                  "the k-group sums fit in the staging tiles");
+    __shared__ __attribute__((aligned(1024))) uint8_t sT[KG][NS][(BP + BM) * ROWB];
     __shared__ float s_code2[kMaxSeg][256];
 
     const BlockTile bt = block_tile(a);
@@ -1117,9 +1184,11 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
     const int64_t s1 = uniform64(s0 + per < a.total_steps ? s0 + per : a.total_steps);
 
     for (int s = 0; s < a.nseg; ++s)
-        for (int i = threadIdx.x; i < 256; i += NT) s_code2[s][i] = code2_entry(a.w[s], i);
+        for (int i = threadIdx.x; i < 256; i += KG * NT) s_code2[s][i] = code2_entry(a.w[s], i);
 
-    const int wave = threadIdx.x >> 6;
+    const int wave_all = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int g = KG > 1 ? wave_all / (WP * WM) : 0;           // k-group
+    const int wave = KG > 1 ? wave_all % (WP * WM) : wave_all;  // wave inside the group
     const int wp = wave % WP, wm = wave / WP;
     const int lane = threadIdx.x & 63;
 
@@ -1130,7 +1199,7 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
         for (int j = 0; j < TM; ++j) acc[i][j] = (float16_t){};
 
     // LoRA slabs: acc += A^T[k rows] . da[m rows]^T (reduction over the rank).
-    if (split == 0) {
+    if (split == 0 && g == 0) {
         const int r = lane & 31, kh = (lane >> 5) * 8;
         for (int s = 0; s < a.nseg; ++s) {
             const LoraDev &lo = a.lora[s];
@@ -1158,21 +1227,28 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
         }
     }
 
+    uint8_t *sW[2] = {sT[g][0], sT[g][1]};
+    uint8_t *sA[2] = {sT[g][0] + BP * ROWB, sT[g][1] + BP * ROWB};
     DxWeight<DT, BP> wt[2] = {};
     ActTile<BM, NT> at[2] = {};
+    int vld[2] = {BR, BR};  // valid dY columns of each register stage
     const rsrc_t ar = act_rsrc<BM>(a, m0);
+    const rsrc_t ar0 = make_rsrc(a.act, 0);
     const ActAddr aa = act_addr<NT>(a.ld_act);
     __syncthreads();  // tables
     // The reduction range [s0, s1) walks the stacked segments in order; each segment runs the
     // forward kernel's pipeline (two register stages, two LDS stages, next tile's staging
-    // interleaved with the MFMAs, no branches in the loop body, odd step after the loop) with
-    // its descriptor held in registers.  A segment's partial last step (rows % 64 != 0) runs
-    // unpipelined after it, with the dY columns past the segment zeroed.
+    // interleaved with the MFMAs, no branches in the loop body, odd step after the loop) over
+    // the group's steps b0 + g + KG v of the segment, with the segment's descriptor held in
+    // registers.  A segment's partial last step (rows % 64 != 0) has its dY columns past the
+    // segment zeroed in registers before they reach LDS; rows past the weight dequantize
+    // from zero bytes and meet those zeros.
     for (int seg = seg_of_step(a, s0); seg < a.nseg && a.step_start[seg] < s1; ++seg) {
         const int64_t first = a.step_start[seg];
         const int64_t b0 = first > s0 ? first : s0;
         const int64_t e0 = a.step_start[seg + 1] < s1 ? a.step_start[seg + 1] : s1;
         if (b0 >= e0) continue;
+        const int64_t nv = (e0 - b0 + KG - 1) / KG;  // the same in every group
         const DevWeight w = a.w[seg];
         const WeightRsrc wr = weight_rsrc(w);
         const WAddr wa = dx_waddr<BP>(wr, p0, K);
@@ -1180,63 +1256,46 @@ __global__ __launch_bounds__(WP *WM * 64) void dx_kernel(const GemmArgs a) {
         const float *code2 = s_code2[seg];
         float code_r[16];
         load_code_sgpr(w.code, code_r);
-        // the step holding the segment's last rows is partial unless rows % 64 == 0
-        const bool partial_last = (w.rows % BR) != 0 && e0 == a.step_start[seg + 1];
-        const int64_t e_full = partial_last ? e0 - 1 : e0;
-        auto stage = [&](ActTile<BM, NT> &t, DxWeight<DT, BP> &u, int64_t st) {
+        auto stage = [&](int b, int64_t v) {
+            const int64_t st = b0 + g + KG * v;
             const int64_t n0 = (st - first) * BR;
-            t.load(ar, aa, static_cast<int>((col_base + n0) * 2));
-            u.load(wr, wa, n0, K);
+            at[b].load(KG > 1 && st >= e0 ? ar0 : ar, aa, static_cast<int>((col_base + n0) * 2));
+            wt[b].load(wr, wa, n0, K);
+            vld[b] = w.rows - n0 < BR ? static_cast<int>(w.rows - n0) : BR;
         };
         __syncthreads();  // the previous segment's last MFMAs have read the LDS stages
-        if (b0 < e_full) {
-            stage(at[0], wt[0], b0);
-            stage(at[1], wt[1], b0 + 1);
-            at[0].store(sA[0]);
-            {
-                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
+        stage(0, 0);
+        stage(1, 1);
+        if (vld[0] < BR) at[0].mask(vld[0]);
+        at[0].store(sA[0]);
+        {
+            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
 #pragma unroll
-                for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
-            }
-            __syncthreads();
-            int64_t st = b0;
-            for (; st + 1 < e_full; st += 2) {
+            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
+        }
+        __syncthreads();
+        int64_t v = 0;
+        for (; v + 1 < nv; v += 2) {
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    stage(at[b], wt[b], st + b + 2);
-                    const Nf4Table tb =
-                        make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
-                    mma_step_dx<DT, BP, TP, TM>(
-                        acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
-                            at[b ^ 1].store_part(sA[b ^ 1], ks);
-                            wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
-                        });
-                    __syncthreads();
-                }
-            }
-            if (st < e_full) {
-                mma_step_dx<DT, BP, TP, TM>(acc, sW[0], sA[0], wp * (BP / WP), wm * (BM / WM),
-                                            [](int) {});
+            for (int b = 0; b < 2; ++b) {
+                stage(b, v + b + 2);
+                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
+                mma_step_dx<DT, BP, TP, TM>(
+                    acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
+                        if (ks == 0 && vld[b ^ 1] < BR) at[b ^ 1].mask(vld[b ^ 1]);
+                        at[b ^ 1].store_part(sA[b ^ 1], ks);
+                        wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                    });
                 __syncthreads();
             }
         }
-        if (partial_last && e_full >= b0) {
-            const int64_t st = e0 - 1;
-            stage(at[0], wt[0], st);
-            at[0].mask(static_cast<int>(w.rows - (st - first) * BR));
-            at[0].store(sA[0]);
-            {
-                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
-#pragma unroll
-                for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
-            }
-            __syncthreads();
+        if (v < nv)
             mma_step_dx<DT, BP, TP, TM>(acc, sW[0], sA[0], wp * (BP / WP), wm * (BM / WM),
                                         [](int) {});
-        }
     }
-    epilogue<DT, TP, TM>(a, acc, p0 + wp * (BP / WP), K, 0, m0 + wm * (BM / WM), split,
-                         bt.nsplit > 1);
+    if constexpr (KG > 1) group_sum<TP, TM, KG, NT>(acc, &sT[0][0][0], g);
+    epilogue<DT, TP, TM, KG>(a, acc, p0 + wp * (BP / WP), K, 0, m0 + wm * (BM / WM), split,
+                             bt.nsplit > 1, g);
 }
 
 // Split reduction over the tail columns [col0, col0 + n_out):
@@ -1288,7 +1347,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial,
 // ------------------------------------------------------------------------------ host side
 
 struct Plan {
-    int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves, 2: small-M path,
+    int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves, 3: 128x128 tile /
+                   // two k-groups of 4 waves, 2: small-M path,
                    // 4: decode path (M <= 16)
     int bp, bm;
     int splits;    // reduction splits of the tail tiles
@@ -1343,9 +1403,11 @@ int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const n
 
 // Tile and split choice by a cost model whose constants were measured on MI355X (fp16, M = 2048,
 // every Qwen2.5-1.5B projection, each plan timed): one 64-deep step of a 256x256 tile takes
-// ~2.45 us with one workgroup per CU; a 128x128 step ~1.15 us alone on a CU and ~1.4 us with two
-// workgroups per CU.  Workgroups run in rounds of 256 (256x256) or 512 (128x128); a last
-// 128x128 round of at most 256 workgroups runs one per CU at the single-workgroup speed.  Split-K adds
+// ~2.45 us with one workgroup per CU; a 128x128 step ~1.4 us with two workgroups per CU.
+// Workgroups run in rounds of 256 (256x256) or 512 (128x128); a last 128x128 round of at most
+// 256 workgroups runs one per CU at the single-workgroup speed (~1.15 us per step).  A single
+// round of 128x128 tiles with one workgroup per CU costs ~7.8 us + 0.93 us per step with 4 waves
+// and ~8.5 us + 0.75 us per step with two k-groups of 4 waves (timed over K).  Split-K adds
 // the fp32 partial round trip (written by the GEMM, read back by the reduction) at ~5 TB/s plus
 // ~12 us of reduction launch and tail.  The larger tile needs 4x fewer dequant instructions per
 // MFMA, which the step times already contain.
@@ -1361,8 +1423,20 @@ double plan_cost(int cfg, int64_t tiles, int64_t mt, int64_t tail_start, int spl
     const int64_t bp = cfg == 0 ? 256 : 128;
     const int64_t full = splits > 1 ? tail_start : tiles;
     const int64_t tail_blocks = splits > 1 ? (tiles - tail_start) * splits : 0;
-    const double t_step = cfg == 0 ? 2.45 : (full + tail_blocks <= kCUs ? 1.15 : 1.4);
     const int64_t per = (steps + splits - 1) / splits;
+    const double split_cost =
+        splits > 1 ? 2.0 * double(splits) * double(m) * double((tiles - tail_start) / mt) *
+                             double(bp) * 4.0 / 5.0e6 + 12.0
+                   : 0.0;
+    if (cfg == 3 || (cfg == 1 && full + tail_blocks <= kCUs)) {
+        // 128x128 tiles, one workgroup per CU in a single round: fixed cost (launch, tables,
+        // first loads, epilogue) plus the longest workgroup's steps, measured with 4 waves and
+        // with two k-groups of 4 waves; the k-groups take no more than one round
+        if (full + tail_blocks > kCUs) return 1e30;
+        const double st = double(full > 0 ? steps : per);
+        return (cfg == 3 ? 0.75 * st + 8.5 : 0.93 * st + 7.8) + split_cost;
+    }
+    const double t_step = cfg == 0 ? 2.45 : 1.4;
     const int64_t rounds = (full + slots - 1) / slots;
     double c = double(rounds) * double(steps) * t_step + 1.0;
     if (cfg == 1 && full > kCUs && full % slots != 0 && full % slots <= kCUs && tail_blocks == 0)
@@ -1370,17 +1444,13 @@ double plan_cost(int cfg, int64_t tiles, int64_t mt, int64_t tail_start, int spl
     const int64_t free_slots = rounds * slots - full;
     if (tail_blocks > free_slots)
         c += double((tail_blocks - free_slots + slots - 1) / slots) * double(per) * t_step;
-    if (splits > 1) {
-        const double tail_cols = double((tiles - tail_start) / mt) * double(bp);
-        c += 2.0 * double(splits) * double(m) * tail_cols * 4.0 / 5.0e6 + 12.0;
-    }
-    return c;
+    return c + split_cost;
 }
 
 Plan make_plan(int64_t m, int64_t big, int64_t small, int64_t steps, int max_splits = kMaxSplits) {
     Plan best{};
     double best_cost = 0.0;
-    for (int cfg = 0; cfg < 2; ++cfg) {
+    for (int cfg : {0, 1, 3}) {
         const int64_t tiles = cfg == 0 ? big : small;
         const int64_t mt = (m + (cfg == 0 ? 255 : 127)) / (cfg == 0 ? 256 : 128);
         for (int s = 1; s <= max_splits; ++s) {
@@ -1439,9 +1509,20 @@ Plan plan_decode(const nf4_weight *ws, int nw) {
 // few rows (sum of rows < K); the tiled GEMMs otherwise (measured at M = 64 on the Qwen2.5-1.5B
 // and -7B projections: q|k|v, o and gate|up 4-30 % faster tiled with split-K, the 1.5B down
 // projection 25 % faster on the small-M kernel).
-Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
-    if (m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
-    if (m <= kGemvMaxM) {
+// A tiling pinned by the caller: tile shape `tile` (0, 1 or 3 as Plan::cfg) with every tile's
+// reduction split `splits` ways (1: none); an empty last split is refused (splits = 0 returned).
+Plan pinned_plan(int tile, int splits, int64_t big, int64_t small, int64_t steps) {
+    if ((tile != 0 && tile != 1 && tile != 3) || splits < 1 || splits > kMaxSplits) return Plan{};
+    const int64_t per = (steps + splits - 1) / splits;
+    if (splits > 1 && (splits - 1) * per >= steps) return Plan{};
+    const int b = tile == 0 ? 256 : 128;
+    const int64_t tiles = tile == 0 ? big : small;
+    return Plan{tile, b, b, splits, tiles, 0, splits > 1 ? 0 : tiles};
+}
+
+Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1) {
+    if (tile < 0 && m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
+    if (tile < 0 && m <= kGemvMaxM) {
         int64_t n = 0;
         for (int i = 0; i < nw; ++i) n += ws[i].rows;
         if (m <= 32 || n < ws[0].cols) return plan_gemv(m, ws, nw);
@@ -1453,15 +1534,17 @@ Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw) {
     }
     big *= (m + 255) / 256;
     small *= (m + 127) / 128;
+    if (tile >= 0) return pinned_plan(tile, splits, big, small, ws[0].cols / BR);
     return make_plan(m, big, small, ws[0].cols / BR);
 }
 
-Plan plan_dx(int64_t m, const nf4_weight *ws, int nw) {
+Plan plan_dx(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1) {
     int64_t steps = 0;
     for (int i = 0; i < nw; ++i) steps += (ws[i].rows + BR - 1) / BR;
     const int64_t K = ws[0].cols;
     const int64_t big = ((K + 255) / 256) * ((m + 255) / 256);
     const int64_t small = ((K + 127) / 128) * ((m + 127) / 128);
+    if (tile >= 0) return pinned_plan(tile, splits, big, small, steps);
     return make_plan(m, big, small, steps);
 }
 
@@ -1487,6 +1570,8 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
         }
     } else if (p.cfg == 0)
         hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
+    else if (p.cfg == 3)
+        hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2, 0, 2>), grid, dim3(512), 0, st, g);
     else
         hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2>), grid, dim3(256), 0, st, g);
     return status_of(hipGetLastError());
@@ -1497,6 +1582,8 @@ int launch_paired(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
     if (p.cfg == 0)
         hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4, EPI>), grid, dim3(512), 0, st, g);
+    else if (p.cfg == 3)
+        hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2, EPI, 2>), grid, dim3(512), 0, st, g);
     else
         hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2, EPI>), grid, dim3(256), 0, st, g);
     return status_of(hipGetLastError());
@@ -1507,6 +1594,8 @@ int launch_dx(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
     if (p.cfg == 0)
         hipLaunchKernelGGL((dx_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
+    else if (p.cfg == 3)
+        hipLaunchKernelGGL((dx_kernel<DT, 128, 128, 2, 2, 2>), grid, dim3(512), 0, st, g);
     else
         hipLaunchKernelGGL((dx_kernel<DT, 128, 128, 2, 2>), grid, dim3(256), 0, st, g);
     return status_of(hipGetLastError());
@@ -1564,10 +1653,10 @@ extern "C" size_t nf4_linear_dx_workspace(int64_t m, const nf4_weight *ws, int n
     return static_cast<size_t>(p.splits) * m * (ws[0].cols - dx_tail_col0(p, m)) * sizeof(float);
 }
 
-extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_weight *ws, int nw,
-                              const void *bias, const nf4_lora *loras, int nlora, void *y,
-                              int64_t ldy, int dtype, void *workspace, size_t workspace_bytes,
-                              void *stream) {
+extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const nf4_weight *ws,
+                                    int nw, const void *bias, const nf4_lora *loras, int nlora,
+                                    void *y, int64_t ldy, int dtype, void *workspace,
+                                    size_t workspace_bytes, void *stream, int tile, int splits) {
     if (dtype != NF4_F16 && dtype != NF4_BF16) return NF4_ERR_ARG;
     if (m < 0 || !y || (m > 0 && !x) || nlora < 0 || (nlora > 0 && !loras)) return NF4_ERR_ARG;
     GemmArgs g;
@@ -1598,7 +1687,8 @@ extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_w
     g.n_out = n_out;
     g.vec_out = aligned(y, 8) && ldy % 4 == 0;
     for (int i = 0; i < nw; ++i) g.vec_out = g.vec_out && (g.seg_off[i] % 4 == 0);
-    const Plan p = plan_fwd(m, ws, nw);
+    const Plan p = plan_fwd(m, ws, nw, tile, splits);
+    if (p.splits == 0) return NF4_ERR_ARG;
     g.splits = p.splits;
     g.per_split = (g.K / BR + p.splits - 1) / p.splits;
     const int64_t bp = p.bp, bm = p.bm;
@@ -1621,10 +1711,18 @@ extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_w
                              : launch_reduce<NF4_F16>(g, p.splits, s);
 }
 
-extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws, int nw,
-                             const nf4_lora *loras, int nlora, void *dx, int64_t lddx,
-                             int accumulate, int dtype, void *workspace, size_t workspace_bytes,
-                             void *stream) {
+extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_weight *ws, int nw,
+                              const void *bias, const nf4_lora *loras, int nlora, void *y,
+                              int64_t ldy, int dtype, void *workspace, size_t workspace_bytes,
+                              void *stream) {
+    return nf4_linear_fwd_tiled(x, m, ldx, ws, nw, bias, loras, nlora, y, ldy, dtype, workspace,
+                                workspace_bytes, stream, NF4_TILE_AUTO, 1);
+}
+
+extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws,
+                                   int nw, const nf4_lora *loras, int nlora, void *dx,
+                                   int64_t lddx, int accumulate, int dtype, void *workspace,
+                                   size_t workspace_bytes, void *stream, int tile, int splits) {
     if (dtype != NF4_F16 && dtype != NF4_BF16) return NF4_ERR_ARG;
     if (m < 0 || !dx || (m > 0 && !dy) || nlora < 0 || (nlora > 0 && !loras)) return NF4_ERR_ARG;
     GemmArgs g;
@@ -1655,7 +1753,8 @@ extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_
     g.n_out = g.K;
     g.accumulate = accumulate != 0;
     g.vec_out = aligned(dx, 8) && lddx % 4 == 0;
-    const Plan p = plan_dx(m, ws, nw);
+    const Plan p = plan_dx(m, ws, nw, tile, splits);
+    if (p.splits == 0) return NF4_ERR_ARG;
     g.splits = p.splits;
     const int64_t bp = p.bp, bm = p.bm;
     g.m_tiles = (m + bm - 1) / bm;
@@ -1679,13 +1778,22 @@ extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_
                              : launch_reduce<NF4_F16>(g, p.splits, s);
 }
 
+extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws, int nw,
+                             const nf4_lora *loras, int nlora, void *dx, int64_t lddx,
+                             int accumulate, int dtype, void *workspace, size_t workspace_bytes,
+                             void *stream) {
+    return nf4_linear_dx_tiled(dy, m, lddy, ws, nw, loras, nlora, dx, lddx, accumulate, dtype,
+                               workspace, workspace_bytes, stream, NF4_TILE_AUTO, 1);
+}
+
 namespace {
 
 // The gate | up pair with the SwiGLU epilogue (forward: out = H [M, I]; backward: aux = dH,
 // out = dG | dU [M, 2I]).  Tiles of the 256x256 or 128x128 forward kernel, chosen by the same
 // cost model over the stacked 2I rows, never split (the epilogue needs whole sums).
 int paired_swiglu(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_up, void *out,
-                  int64_t ldo, const void *aux, int64_t ld_aux, int dtype, bool bwd, void *stream) {
+                  int64_t ldo, const void *aux, int64_t ld_aux, int dtype, bool bwd, void *stream,
+                  int tile = NF4_TILE_AUTO) {
     if (dtype != NF4_F16 && dtype != NF4_BF16) return NF4_ERR_ARG;
     if (m < 0 || !out || (m > 0 && !x) || (bwd && m > 0 && !aux)) return NF4_ERR_ARG;
     GemmArgs g;
@@ -1705,7 +1813,9 @@ int paired_swiglu(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_
                 (!bwd || (inter % 4 == 0 && aligned(aux, 8) && ld_aux % 4 == 0));
     const int64_t big = ((inter + 127) / 128) * ((m + 255) / 256);
     const int64_t small = ((inter + 63) / 64) * ((m + 127) / 128);
-    const Plan p = make_plan(m, big, small, g.K / BR, 1);
+    const Plan p = tile < 0 ? make_plan(m, big, small, g.K / BR, 1)
+                            : pinned_plan(tile, 1, big, small, g.K / BR);
+    if (p.splits == 0) return NF4_ERR_ARG;
     g.splits = 1;
     g.per_split = g.K / BR;
     g.m_tiles = (m + p.bm - 1) / p.bm;
@@ -1731,4 +1841,12 @@ extern "C" int nf4_linear_swiglu_bwd(const void *x, int64_t m, int64_t ldx,
                                      const nf4_weight *gate_up, const void *dh, int64_t lddh,
                                      void *dgu, int64_t lddgu, int dtype, void *stream) {
     return paired_swiglu(x, m, ldx, gate_up, dgu, lddgu, dh, lddh, dtype, true, stream);
+}
+
+extern "C" int nf4_linear_swiglu_tiled(const void *x, int64_t m, int64_t ldx,
+                                       const nf4_weight *gate_up, void *out, int64_t ldo,
+                                       const void *dh, int64_t lddh, int dtype, void *stream,
+                                       int backward, int tile) {
+    return paired_swiglu(x, m, ldx, gate_up, out, ldo, dh, lddh, dtype, backward != 0, stream,
+                         tile);
 }

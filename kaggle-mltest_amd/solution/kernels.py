@@ -14,6 +14,9 @@ from .quant_state import weight_array, weight_desc
 
 GEMM_DTYPES = (torch.float16, torch.bfloat16)
 
+# tilings of the tiled GEMMs (NF4_TILE_* of the C header)
+TILE_256, TILE_128, TILE_128_KSPLIT2 = 0, 1, 3
+
 
 def _code(dtype: torch.dtype, allowed=GEMM_DTYPES) -> int:
     if dtype not in allowed:
@@ -79,9 +82,11 @@ def _lora_array(loras):
 
 
 def linear_fwd(x: torch.Tensor, weights, bias: torch.Tensor | None = None, loras=(),
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, tile: int | None = None,
+               splits: int = 1) -> torch.Tensor:
     """Y[M, sum rows] = x[M, K] @ W_stack^T (+ bias) (+ LoRA terms).  `loras`: NF4Lora structs
-    whose pointers stay alive for the call (the caller keeps the tensors)."""
+    whose pointers stay alive for the call (the caller keeps the tensors).  `tile` (TILE_*)
+    and `splits` pin the tiling; None lets the library choose."""
     _check_device(x, bias)
     dt = _code(x.dtype)
     m, k = x.shape
@@ -90,20 +95,27 @@ def linear_fwd(x: torch.Tensor, weights, bias: torch.Tensor | None = None, loras
         out = torch.empty((m, n), dtype=x.dtype, device=x.device)
     arr = _descs(weights)
     lib = load()
-    ws_bytes = lib.nf4_linear_fwd_workspace(m, arr, len(weights), dt)
+    if tile is None:
+        ws_bytes = lib.nf4_linear_fwd_workspace(m, arr, len(weights), dt)
+    else:
+        ws_bytes = 4 * splits * m * n if splits > 1 else 0
     ws = _workspace(ws_bytes, x.device)
     larr, nl = _lora_array(loras)
-    st = lib.nf4_linear_fwd(x.data_ptr() if m else None, m, x.stride(0), arr, len(weights),
-                            bias.data_ptr() if bias is not None else None, larr, nl,
-                            out.data_ptr(), out.stride(0), dt,
-                            ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(x))
-    check(st, "nf4_linear_fwd")
+    args = (x.data_ptr() if m else None, m, x.stride(0), arr, len(weights),
+            bias.data_ptr() if bias is not None else None, larr, nl, out.data_ptr(),
+            out.stride(0), dt, ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(x))
+    if tile is None:
+        check(lib.nf4_linear_fwd(*args), "nf4_linear_fwd")
+    else:
+        check(lib.nf4_linear_fwd_tiled(*args, int(tile), int(splits)), "nf4_linear_fwd_tiled")
     return out
 
 
 def linear_dx(dy: torch.Tensor, weights, loras=(), out: torch.Tensor | None = None,
-              accumulate: bool = False) -> torch.Tensor:
-    """dX[M, K] (+)= dY[M, sum rows] @ W_stack (+ LoRA terms)."""
+              accumulate: bool = False, tile: int | None = None,
+              splits: int = 1) -> torch.Tensor:
+    """dX[M, K] (+)= dY[M, sum rows] @ W_stack (+ LoRA terms); `tile` / `splits` as in
+    linear_fwd."""
     _check_device(dy)
     dt = _code(dy.dtype)
     m = dy.shape[0]
@@ -113,13 +125,19 @@ def linear_dx(dy: torch.Tensor, weights, loras=(), out: torch.Tensor | None = No
         accumulate = False
     arr = _descs(weights)
     lib = load()
-    ws_bytes = lib.nf4_linear_dx_workspace(m, arr, len(weights), dt)
+    if tile is None:
+        ws_bytes = lib.nf4_linear_dx_workspace(m, arr, len(weights), dt)
+    else:
+        ws_bytes = 4 * splits * m * k if splits > 1 else 0
     ws = _workspace(ws_bytes, dy.device)
     larr, nl = _lora_array(loras)
-    st = lib.nf4_linear_dx(dy.data_ptr() if m else None, m, dy.stride(0), arr, len(weights),
-                           larr, nl, out.data_ptr(), out.stride(0), int(accumulate), dt,
-                           ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(dy))
-    check(st, "nf4_linear_dx")
+    args = (dy.data_ptr() if m else None, m, dy.stride(0), arr, len(weights), larr, nl,
+            out.data_ptr(), out.stride(0), int(accumulate), dt,
+            ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(dy))
+    if tile is None:
+        check(lib.nf4_linear_dx(*args), "nf4_linear_dx")
+    else:
+        check(lib.nf4_linear_dx_tiled(*args, int(tile), int(splits)), "nf4_linear_dx_tiled")
     return out
 
 
@@ -170,15 +188,22 @@ def _pair(gate, up):
     return _descs([gate, up])
 
 
-def linear_swiglu_fwd(x: torch.Tensor, gate, up, out: torch.Tensor | None = None) -> torch.Tensor:
+def linear_swiglu_fwd(x: torch.Tensor, gate, up, out: torch.Tensor | None = None,
+                      tile: int | None = None) -> torch.Tensor:
     """H[M, I] = silu(x @ Wg^T) * (x @ Wu^T), the SwiGLU step in the gate|up GEMM's epilogue.
-    `gate`, `up`: (packed, quant_state) pairs of equal shape [I, K]."""
+    `gate`, `up`: (packed, quant_state) pairs of equal shape [I, K]; `tile` pins the tiling."""
     _check_device(x)
     m = x.shape[0]
     inter = int(gate[1].shape[0])
     if out is None:
         out = torch.empty((m, inter), dtype=x.dtype, device=x.device)
     arr = _pair(gate, up)
+    if tile is not None:
+        st = load().nf4_linear_swiglu_tiled(x.data_ptr() if m else None, m, x.stride(0), arr,
+                                            out.data_ptr(), out.stride(0), None, 0,
+                                            _code(x.dtype), stream_of(x), 0, int(tile))
+        check(st, "nf4_linear_swiglu_tiled")
+        return out
     st = load().nf4_linear_swiglu_fwd(x.data_ptr() if m else None, m, x.stride(0), arr,
                                       out.data_ptr(), out.stride(0), _code(x.dtype), stream_of(x))
     check(st, "nf4_linear_swiglu_fwd")
@@ -186,7 +211,7 @@ def linear_swiglu_fwd(x: torch.Tensor, gate, up, out: torch.Tensor | None = None
 
 
 def linear_swiglu_bwd(x: torch.Tensor, gate, up, d_hidden: torch.Tensor,
-                      out: torch.Tensor | None = None) -> torch.Tensor:
+                      out: torch.Tensor | None = None, tile: int | None = None) -> torch.Tensor:
     """dGU[M, 2I] (dgate | dup) from d_hidden [M, I] and gate/up recomputed from x inside the
     GEMM; the input of linear_dx over the stacked (gate, up) pair."""
     _check_device(x, d_hidden)
@@ -197,6 +222,13 @@ def linear_swiglu_bwd(x: torch.Tensor, gate, up, d_hidden: torch.Tensor,
     if out is None:
         out = torch.empty((m, 2 * inter), dtype=x.dtype, device=x.device)
     arr = _pair(gate, up)
+    if tile is not None:
+        st = load().nf4_linear_swiglu_tiled(x.data_ptr() if m else None, m, x.stride(0), arr,
+                                            out.data_ptr(), out.stride(0), d_hidden.data_ptr(),
+                                            d_hidden.stride(0), _code(x.dtype), stream_of(x), 1,
+                                            int(tile))
+        check(st, "nf4_linear_swiglu_tiled")
+        return out
     st = load().nf4_linear_swiglu_bwd(x.data_ptr() if m else None, m, x.stride(0), arr,
                                       d_hidden.data_ptr(), d_hidden.stride(0), out.data_ptr(),
                                       out.stride(0), _code(x.dtype), stream_of(x))
