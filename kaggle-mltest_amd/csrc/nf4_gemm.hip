@@ -55,6 +55,15 @@ struct LoraDev {
     int has;
 };
 
+// Tile decomposition of one part of a launch: tiles run segment by segment (forward) with m
+// fastest; a two-part launch (head + tail plans) holds one map per part.
+struct TileMap {
+    int64_t m_tiles;
+    int64_t tile_start[kMaxSeg + 1];  // forward: cumulative (p tiles x m tiles) per segment
+    int64_t row0[kMaxSeg];            // forward: first row of each segment the part covers
+    int64_t col0;                     // dx: first output column the part covers
+};
+
 struct GemmArgs {
     const uint16_t *act;          // X (forward) or dY (dx)
     int64_t ld_act;
@@ -63,7 +72,8 @@ struct GemmArgs {
     int64_t K;                    // in_features of every segment
     DevWeight w[kMaxSeg];
     int64_t seg_off[kMaxSeg];     // forward: output column offset; dx: dY column offset
-    int64_t tile_start[kMaxSeg + 1];  // forward: cumulative (p tiles x m tiles) per segment
+    TileMap map[2];               // [1]: the second part of a two-part launch
+    int64_t blocks0;              // two-part launch: workgroups of the first part (else 0)
     int64_t step_start[kMaxSeg + 1];  // dx: cumulative reduction steps per segment
     int nseg;
     LoraDev lora[kMaxSeg];
@@ -80,8 +90,6 @@ struct GemmArgs {
     int64_t tail_start;
     int64_t tail_col0;
     int64_t tail_cols;
-    int64_t m_tiles;
-    int64_t p_tiles;              // dx: tiles along K
     int64_t total_steps;          // dx: sum of step counts
     int accumulate;               // dx: add into out
     int vec_out;                  // 8-byte output stores allowed (paired: and aux loads)
@@ -125,11 +133,11 @@ __device__ __forceinline__ uint16_t from_f32(float v) {
     else return __builtin_bit_cast(uint16_t, static_cast<half_t>(v));
 }
 
-__device__ __forceinline__ int seg_of_tile(const GemmArgs &a, int64_t t) {
+__device__ __forceinline__ int seg_of_tile(const GemmArgs &a, const TileMap &tm, int64_t t) {
     int s = 0;
 #pragma unroll
     for (int i = 1; i < kMaxSeg; ++i)
-        if (i < a.nseg && t >= a.tile_start[i]) s = i;
+        if (i < a.nseg && t >= tm.tile_start[i]) s = i;
     return s;
 }
 
@@ -158,8 +166,7 @@ struct BlockTile {
     int nsplit;
 };
 
-__device__ __forceinline__ BlockTile block_tile(const GemmArgs &a) {
-    const uint32_t b = blockIdx.x;
+__device__ __forceinline__ BlockTile block_tile(const GemmArgs &a, uint32_t b) {
     const uint32_t ts = static_cast<uint32_t>(a.tail_start);
     if (b < ts) return BlockTile{b, 0, 1};
     const uint32_t r = b - ts, sp = static_cast<uint32_t>(a.splits);
@@ -698,8 +705,16 @@ __device__ __forceinline__ void group_sum(float16_t (&acc)[TP][TM], uint8_t *lds
 // covers BP / 2 rows j of both weights, gate in the first half of its W tile (dequantized by
 // the first half of the waves) and up in the second, no bias, LoRA or split.  KG k-groups
 // (group_sum above) split each tile's reduction inside the workgroup.
-template <int DT, int BP, int BM, int WP, int WM, int EPI = 0, int KG = 1>
-__global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) {
+template <int BP, int BM, int KG>
+constexpr int stage_bytes() {  // LDS of the staging tiles: KG groups x 2 stages x (W + act)
+    return KG * 2 * (BP + BM) * ROWB;
+}
+
+// One workgroup of the forward GEMM: block `blk` of part `tm` of the launch, staging tiles in
+// `lds` (stage_bytes<BP, BM, KG>() bytes), code2 tables in `s_code2`.
+template <int DT, int BP, int BM, int WP, int WM, int EPI, int KG>
+__device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, uint32_t blk,
+                                         uint8_t *lds, float (*s_code2)[256]) {
     constexpr int NT = WP * WM * 64;  // threads of one k-group
     constexpr int TP = BP / WP / 32, TM = BM / WM / 32;
     constexpr bool PAIR = EPI != 0;
@@ -707,20 +722,20 @@ __global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) 
     static_assert(NT == 2 * BP, "forward weight tile mapping needs 2 threads per row");
     static_assert(!PAIR || TP % 2 == 0, "paired tiles split each wave's fragments in halves");
     constexpr int NS = 2;  // LDS stages per k-group
-    static_assert(KG == 1 || BP * BM * 4 <= KG * NS * (BP + BM) * ROWB,
+    static_assert(KG == 1 || BP * BM * 4 <= stage_bytes<BP, BM, KG>(),
                   "the k-group sums fit in the staging tiles");
-    __shared__ __attribute__((aligned(1024))) uint8_t sT[KG][NS][(BP + BM) * ROWB];
-    __shared__ float s_code2[PAIR ? 2 : 1][256];
+    auto sT = reinterpret_cast<uint8_t(*)[NS][(BP + BM) * ROWB]>(lds);
 
     // tiles: segments in order, m fastest.  32-bit tile arithmetic: 64-bit divisions are long
     // scalar sequences the whole CU waits on.
-    const BlockTile bt = block_tile(a);
+    const BlockTile bt = block_tile(a, blk);
     const int split = bt.split;
     const int64_t tile = bt.tile;
-    const int seg = PAIR ? 0 : seg_of_tile(a, tile);
-    const uint32_t local = static_cast<uint32_t>(tile - a.tile_start[seg]);
-    const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
-    const int64_t p0 = uniform64(static_cast<int64_t>(local / mtl) * (PAIR ? PH : BP));
+    const int seg = PAIR ? 0 : seg_of_tile(a, tm, tile);
+    const uint32_t local = static_cast<uint32_t>(tile - tm.tile_start[seg]);
+    const uint32_t mtl = static_cast<uint32_t>(tm.m_tiles);
+    const int64_t p0 =
+        uniform64(tm.row0[seg] + static_cast<int64_t>(local / mtl) * (PAIR ? PH : BP));
     const int64_t m0 = uniform64(static_cast<int64_t>(local % mtl) * BM);
     const int wave_all = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int g = KG > 1 ? wave_all / (WP * WM) : 0;           // k-group
@@ -843,6 +858,28 @@ __global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) 
                                  split, bt.nsplit > 1, g);
 }
 
+template <int DT, int BP, int BM, int WP, int WM, int EPI = 0, int KG = 1>
+__global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<BP, BM, KG>()];
+    __shared__ float s_code2[EPI != 0 ? 2 : 1][256];
+    fwd_body<DT, BP, BM, WP, WM, EPI, KG>(a, a.map[0], blockIdx.x, lds, s_code2);
+}
+
+// A two-part launch: workgroups [0, blocks0) run 256x256 tiles over the first part's map, the
+// rest 128x128 tiles with two k-groups over the second part's (both 512 threads, the same
+// staging LDS), so that the second part's workgroups start on the CUs the first part frees.
+template <int DT, int EPI>
+__global__ __launch_bounds__(512) void fwd_head_tail_kernel(const GemmArgs a) {
+    static_assert(stage_bytes<256, 256, 1>() == stage_bytes<128, 128, 2>(), "one LDS layout");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
+    __shared__ float s_code2[EPI != 0 ? 2 : 1][256];
+    const uint32_t b0 = static_cast<uint32_t>(a.blocks0);
+    if (blockIdx.x < b0)
+        fwd_body<DT, 256, 256, 2, 4, EPI, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
+    else
+        fwd_body<DT, 128, 128, 2, 2, EPI, 2>(a, a.map[1], blockIdx.x - b0, lds, s_code2);
+}
+
 // ------------------------------------------------------------------------ decode forward path
 //
 // Y = X W^T for M <= 16 tokens with K a multiple of 128 (decode), bound by the dequant VALU work
@@ -890,8 +927,8 @@ void decode_kernel(const GemmArgs a) {
     __shared__ float4_t s_red[NW > 1 ? NW - 1 : 1][64];
 
     const int64_t tile = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(blockIdx.x));
-    const int seg = seg_of_tile(a, tile);
-    const int64_t p0 = uniform64((tile - a.tile_start[seg]) * 16);
+    const int seg = seg_of_tile(a, a.map[0], tile);
+    const int64_t p0 = uniform64((tile - a.map[0].tile_start[seg]) * 16);
     const DevWeight w = a.w[seg];
     const int64_t K = a.K;
     const int ss = static_cast<int>(K / DK);
@@ -1019,11 +1056,11 @@ void gemv_kernel(const GemmArgs a) {
     __shared__ float s_code2[256];
     __shared__ float4_t s_red[NW / 2][MT * 4][64];
 
-    const BlockTile bt = block_tile(a);
+    const BlockTile bt = block_tile(a, blockIdx.x);
     const int split = bt.split;
     const int64_t tile = bt.tile;
-    const int seg = seg_of_tile(a, tile);
-    const int64_t p0 = (tile - a.tile_start[seg]) * 32;
+    const int seg = seg_of_tile(a, a.map[0], tile);
+    const int64_t p0 = (tile - a.map[0].tile_start[seg]) * 32;
     const DevWeight w = a.w[seg];
     const int64_t K = a.K;
     const int64_t steps = K / BR;
@@ -1161,22 +1198,23 @@ void gemv_kernel(const GemmArgs a) {
     }
 }
 
-template <int DT, int BP, int BM, int WP, int WM, int KG = 1>
-__global__ __launch_bounds__(KG *WP *WM * 64) void dx_kernel(const GemmArgs a) {
+// One workgroup of the input-gradient GEMM (as fwd_body).
+template <int DT, int BP, int BM, int WP, int WM, int KG>
+__device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, uint32_t blk,
+                                        uint8_t *lds, float (*s_code2)[256]) {
     constexpr int NT = WP * WM * 64;  // threads of one k-group
     constexpr int TP = BP / WP / 32, TM = BM / WM / 32;
     static_assert(NT == 2 * BP, "dX weight tile mapping needs 2 threads per k column group");
     constexpr int NS = 2;  // LDS stages per k-group
-    static_assert(KG == 1 || BP * BM * 4 <= KG * NS * (BP + BM) * ROWB,
+    static_assert(KG == 1 || BP * BM * 4 <= stage_bytes<BP, BM, KG>(),
                   "the k-group sums fit in the staging tiles");
-    __shared__ __attribute__((aligned(1024))) uint8_t sT[KG][NS][(BP + BM) * ROWB];
-    __shared__ float s_code2[kMaxSeg][256];
+    auto sT = reinterpret_cast<uint8_t(*)[NS][(BP + BM) * ROWB]>(lds);
 
-    const BlockTile bt = block_tile(a);
+    const BlockTile bt = block_tile(a, blk);
     const int split = bt.split;
     const uint32_t tile = static_cast<uint32_t>(bt.tile);
-    const uint32_t mtl = static_cast<uint32_t>(a.m_tiles);
-    const int64_t p0 = uniform64(static_cast<int64_t>(tile / mtl) * BP);
+    const uint32_t mtl = static_cast<uint32_t>(tm.m_tiles);
+    const int64_t p0 = uniform64(tm.col0 + static_cast<int64_t>(tile / mtl) * BP);
     const int64_t m0 = uniform64(static_cast<int64_t>(tile % mtl) * BM);
     const int64_t K = a.K;
     const int64_t per = bt.nsplit > 1 ? a.per_split : a.total_steps;
@@ -1298,6 +1336,26 @@ __global__ __launch_bounds__(KG *WP *WM * 64) void dx_kernel(const GemmArgs a) {
                              bt.nsplit > 1, g);
 }
 
+template <int DT, int BP, int BM, int WP, int WM, int KG = 1>
+__global__ __launch_bounds__(KG *WP *WM * 64) void dx_kernel(const GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<BP, BM, KG>()];
+    __shared__ float s_code2[kMaxSeg][256];
+    dx_body<DT, BP, BM, WP, WM, KG>(a, a.map[0], blockIdx.x, lds, s_code2);
+}
+
+// Two-part input-gradient launch (as fwd_head_tail_kernel): output columns of the first part
+// in 256x256 tiles, the rest in 128x128 tiles with two k-groups.
+template <int DT>
+__global__ __launch_bounds__(512) void dx_head_tail_kernel(const GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
+    __shared__ float s_code2[kMaxSeg][256];
+    const uint32_t b0 = static_cast<uint32_t>(a.blocks0);
+    if (blockIdx.x < b0)
+        dx_body<DT, 256, 256, 2, 4, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
+    else
+        dx_body<DT, 128, 128, 2, 2, 2>(a, a.map[1], blockIdx.x - b0, lds, s_code2);
+}
+
 // Split reduction over the tail columns [col0, col0 + n_out):
 // out[m][col0 + c] = sum_s partial[s][m][c] (+ bias[col0 + c]) (+ out[m][col0 + c]) in split
 // order (deterministic).  Grid: x = groups of 1024 columns (4 per thread), y = rows.
@@ -1355,6 +1413,10 @@ struct Plan {
     int64_t tiles;
     int waves;     // small-M and decode paths: waves per workgroup
     int64_t tail_start;  // first split tile (tiles before it run whole)
+    // > 0: two launches, whole rounds of 256x256 tiles over the first head_ptiles p-tiles (rows
+    // of the stacked weights forward, columns of dX backward), then the rest in unsplit 128x128
+    // tiles of tiling `cfg` (1 or 3); `tiles` then counts the second launch's tiles (estimate).
+    int64_t head_ptiles;
 
     int64_t blocks() const { return tail_start + (tiles - tail_start) * splits; }
 };
@@ -1412,6 +1474,7 @@ int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const n
 // ~12 us of reduction launch and tail.  The larger tile needs 4x fewer dequant instructions per
 // MFMA, which the step times already contain.
 constexpr int kMaxSplits = 16;
+constexpr double kLaunchGap = 2.0;  // us between two dependent launches on one stream
 
 // Time of a plan: workgroups are dispatched in order into `slots` places (one per CU for the
 // 256x256 tile, two for 128x128).  The whole tiles run in rounds; the split tail tiles' shorter
@@ -1464,6 +1527,23 @@ Plan make_plan(int64_t m, int64_t big, int64_t small, int64_t steps, int max_spl
                                 s > 1 ? ts : tiles};
                     best_cost = c;
                 }
+            }
+        }
+    }
+    // Head + tail: r whole rounds of 256x256 tiles, then the rows (columns) left in one
+    // unsplit launch of 128x128 tiles; each 256-row p-tile of the head removes two 128-row
+    // p-tiles from the tail (an estimate where a segment ends inside a p-tile).
+    const int64_t mt0 = (m + 255) / 256, mt1 = (m + 127) / 128;
+    for (int64_t r = 1; r * kCUs < big; ++r) {
+        const int64_t hp = r * kCUs / mt0;
+        const int64_t tail = small - 2 * hp * mt1;
+        if (hp <= 0 || hp * mt0 >= big || tail <= 0) continue;
+        const double head = plan_cost(0, hp * mt0, mt0, hp * mt0, 1, steps, m);
+        for (int cfg : {1, 3}) {
+            const double c = head + plan_cost(cfg, tail, mt1, tail, 1, steps, m) + kLaunchGap;
+            if (c < best_cost) {
+                best = Plan{cfg, 128, 128, 1, tail, 0, tail, hp};
+                best_cost = c;
             }
         }
     }
@@ -1616,6 +1696,47 @@ int launch_reduce(const GemmArgs &g, int splits, hipStream_t st) {
 
 // First output column of the split tail tiles (output columns: the segments' rows stacked; each
 // segment's tiles run p-tile by p-tile with m fastest).
+// The two parts of a head + tail plan over stacked rows (forward; `unit0` / `unit1` rows per
+// p-tile of the 256x256 and 128x128 tiles: 256 / 128, or 128 / 64 for paired gate | up tiles):
+// the first head_ptiles p-tiles in segment order, then each segment's remaining rows from row0.
+// Returns the number of workgroups of the two-part launch.
+int64_t head_tail_rows(GemmArgs &g, const Plan &p, const int64_t *rows, int nw, int64_t m,
+                       int64_t unit0, int64_t unit1) {
+    TileMap &ha = g.map[0], &tb = g.map[1];
+    ha.m_tiles = (m + 255) / 256;
+    tb.m_tiles = (m + 127) / 128;
+    ha.tile_start[0] = tb.tile_start[0] = 0;
+    int64_t left = p.head_ptiles;
+    for (int i = 0; i < nw; ++i) {
+        const int64_t pt = (rows[i] + unit0 - 1) / unit0;
+        const int64_t take = left < pt ? left : pt;
+        left -= take;
+        const int64_t head_rows = take * unit0 < rows[i] ? take * unit0 : rows[i];
+        ha.row0[i] = 0;
+        tb.row0[i] = head_rows;
+        ha.tile_start[i + 1] = ha.tile_start[i] + take * ha.m_tiles;
+        tb.tile_start[i + 1] =
+            tb.tile_start[i] + ((rows[i] - head_rows + unit1 - 1) / unit1) * tb.m_tiles;
+    }
+    g.blocks0 = ha.tile_start[nw];
+    g.tail_start = int64_t(1) << 31;  // no split tiles in either part
+    return g.blocks0 + tb.tile_start[nw];
+}
+
+// The same for dX over output columns: [0, 256 head_ptiles) in 256x256 tiles, the rest in
+// 128x128 tiles from col0.
+int64_t head_tail_cols(GemmArgs &g, const Plan &p, int64_t m) {
+    TileMap &ha = g.map[0], &tb = g.map[1];
+    const int64_t c0 = p.head_ptiles * 256 < g.K ? p.head_ptiles * 256 : g.K;
+    ha.m_tiles = (m + 255) / 256;
+    tb.m_tiles = (m + 127) / 128;
+    ha.col0 = 0;
+    tb.col0 = c0;
+    g.blocks0 = (c0 / 256) * ha.m_tiles;
+    g.tail_start = int64_t(1) << 31;
+    return g.blocks0 + ((g.K - c0 + 127) / 128) * tb.m_tiles;
+}
+
 int64_t fwd_tail_col0(const Plan &p, int64_t m, const nf4_weight *ws, int nw) {
     const int64_t mt = (m + p.bm - 1) / p.bm;
     int64_t t = 0, col = 0;
@@ -1692,10 +1813,11 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
     g.splits = p.splits;
     g.per_split = (g.K / BR + p.splits - 1) / p.splits;
     const int64_t bp = p.bp, bm = p.bm;
-    g.m_tiles = (m + bm - 1) / bm;
-    g.tile_start[0] = 0;
+    g.map[0].m_tiles = (m + bm - 1) / bm;
+    g.map[0].tile_start[0] = 0;
     for (int i = 0; i < nw; ++i)
-        g.tile_start[i + 1] = g.tile_start[i] + ((ws[i].rows + bp - 1) / bp) * g.m_tiles;
+        g.map[0].tile_start[i + 1] =
+            g.map[0].tile_start[i] + ((ws[i].rows + bp - 1) / bp) * g.map[0].m_tiles;
     hipStream_t s = static_cast<hipStream_t>(stream);
     g.tail_start = p.tail_start;
     g.tail_col0 = p.splits > 1 ? fwd_tail_col0(p, m, ws, nw) : n_out;
@@ -1704,6 +1826,16 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
         const size_t need = static_cast<size_t>(p.splits) * m * g.tail_cols * sizeof(float);
         if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
         g.partial = static_cast<float *>(workspace);
+    }
+    if (p.head_ptiles > 0) {
+        int64_t rows[kMaxSeg];
+        for (int i = 0; i < nw; ++i) rows[i] = ws[i].rows;
+        const dim3 grid(static_cast<unsigned>(head_tail_rows(g, p, rows, nw, m, 256, 128)));
+        if (dtype == NF4_BF16)
+            hipLaunchKernelGGL((fwd_head_tail_kernel<NF4_BF16, 0>), grid, dim3(512), 0, s, g);
+        else
+            hipLaunchKernelGGL((fwd_head_tail_kernel<NF4_F16, 0>), grid, dim3(512), 0, s, g);
+        return status_of(hipGetLastError());
     }
     st = dtype == NF4_BF16 ? launch_fwd<NF4_BF16>(g, p, s) : launch_fwd<NF4_F16>(g, p, s);
     if (st != NF4_OK || p.splits <= 1) return st;
@@ -1757,8 +1889,7 @@ extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, cons
     if (p.splits == 0) return NF4_ERR_ARG;
     g.splits = p.splits;
     const int64_t bp = p.bp, bm = p.bm;
-    g.m_tiles = (m + bm - 1) / bm;
-    g.p_tiles = (g.K + bp - 1) / bp;
+    g.map[0].m_tiles = (m + bm - 1) / bm;
     g.step_start[0] = 0;
     for (int i = 0; i < nw; ++i) g.step_start[i + 1] = g.step_start[i] + (ws[i].rows + BR - 1) / BR;
     g.total_steps = g.step_start[nw];
@@ -1771,6 +1902,14 @@ extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, cons
         const size_t need = static_cast<size_t>(p.splits) * m * g.tail_cols * sizeof(float);
         if (!workspace || workspace_bytes < need) return NF4_ERR_WORKSPACE;
         g.partial = static_cast<float *>(workspace);
+    }
+    if (p.head_ptiles > 0) {
+        const dim3 grid(static_cast<unsigned>(head_tail_cols(g, p, m)));
+        if (dtype == NF4_BF16)
+            hipLaunchKernelGGL((dx_head_tail_kernel<NF4_BF16>), grid, dim3(512), 0, s, g);
+        else
+            hipLaunchKernelGGL((dx_head_tail_kernel<NF4_F16>), grid, dim3(512), 0, s, g);
+        return status_of(hipGetLastError());
     }
     st = dtype == NF4_BF16 ? launch_dx<NF4_BF16>(g, p, s) : launch_dx<NF4_F16>(g, p, s);
     if (st != NF4_OK || p.splits <= 1) return st;
@@ -1818,12 +1957,23 @@ int paired_swiglu(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_
     if (p.splits == 0) return NF4_ERR_ARG;
     g.splits = 1;
     g.per_split = g.K / BR;
-    g.m_tiles = (m + p.bm - 1) / p.bm;
-    g.tile_start[0] = 0;
-    g.tile_start[1] = p.tiles;
+    g.map[0].m_tiles = (m + p.bm - 1) / p.bm;
+    g.map[0].tile_start[0] = 0;
+    g.map[0].tile_start[1] = p.tiles;
     g.tail_start = p.tiles;
     g.tail_col0 = g.n_out;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p.head_ptiles > 0) {
+        const dim3 grid(static_cast<unsigned>(head_tail_rows(g, p, &inter, 1, m, 128, 64)));
+        if (dtype == NF4_BF16) {
+            if (bwd) hipLaunchKernelGGL((fwd_head_tail_kernel<NF4_BF16, 2>), grid, dim3(512), 0, s, g);
+            else hipLaunchKernelGGL((fwd_head_tail_kernel<NF4_BF16, 1>), grid, dim3(512), 0, s, g);
+        } else {
+            if (bwd) hipLaunchKernelGGL((fwd_head_tail_kernel<NF4_F16, 2>), grid, dim3(512), 0, s, g);
+            else hipLaunchKernelGGL((fwd_head_tail_kernel<NF4_F16, 1>), grid, dim3(512), 0, s, g);
+        }
+        return status_of(hipGetLastError());
+    }
     if (dtype == NF4_BF16)
         return bwd ? launch_paired<NF4_BF16, 2>(g, p, s) : launch_paired<NF4_BF16, 1>(g, p, s);
     return bwd ? launch_paired<NF4_F16, 2>(g, p, s) : launch_paired<NF4_F16, 1>(g, p, s);

@@ -123,3 +123,30 @@ def test_tiling_arguments(cuda):
             kernels.linear_fwd(x, [(p, qs)], tile=tile, splits=splits)
     with pytest.raises(NF4LibraryError):
         kernels.linear_dx(_x(8, 64, 2, cuda), [(p, qs)], tile=1, splits=2)
+
+
+def test_head_tail_plans_bit_exact(cuda):
+    """At M = 2048 the cost model runs the stacked gate | up forward and the down projection's
+    input gradient as two launches (whole rounds of 256x256 tiles, then the remaining rows or
+    columns in 128x128 tiles; the gate | up split falls inside the up weight).  One-hot
+    activation rows (row r selects k = r mod K) return weight columns exactly, so every output
+    of both launches is checked bit for bit.  (The SwiGLU pair at this shape takes the same
+    plan; test_swiglu_epilogue holds it to the path's tolerance.)"""
+    from solution import kernels
+
+    banner("head + tail plans", 2048)
+    m, k, inter = 2048, 1536, 8960
+    gate = random_weight(inter, k, seed=501, dev=cuda)
+    up = random_weight(inter, k, seed=502, dev=cuda)
+    w = torch.cat([oracle_w16(*gate), oracle_w16(*up)]).view(torch.int16)
+    onehot = torch.zeros(m, k, dtype=torch.float16, device=cuda)
+    onehot[torch.arange(m), torch.arange(m) % k] = 1.0
+    y = kernels.linear_fwd(onehot, [gate, up]).cpu().view(torch.int16)
+    assert torch.equal(y, w[:, torch.arange(m) % k].t().contiguous())
+
+    down = random_weight(k, inter, seed=503, dev=cuda)
+    wd = oracle_w16(*down).view(torch.int16)
+    dy = torch.zeros(m, k, dtype=torch.float16, device=cuda)
+    dy[torch.arange(m), torch.arange(m) % k] = 1.0
+    dx = kernels.linear_dx(dy, [down]).cpu().view(torch.int16)
+    assert torch.equal(dx, wd[torch.arange(m) % k])
