@@ -53,6 +53,7 @@ struct LoraDev {
     float scale;
     int rank;
     int has;
+    int vec;             // rank % 8 == 0 and 16-byte aligned rows: 16-byte fragment loads
 };
 
 // Tile decomposition of one part of a launch: tiles run segment by segment (forward) with m
@@ -373,6 +374,13 @@ __device__ __forceinline__ u32x4_t gather8(const uint16_t *src, int64_t stride, 
     v.z = e[4] | (uint32_t(e[5]) << 16);
     v.w = e[6] | (uint32_t(e[7]) << 16);
     return v;
+}
+
+// 8 consecutive 16-bit values of a LoRA row (src[0 .. lim)): one 16-byte load when the rows
+// allow it (`vec`), else element by element.
+__device__ __forceinline__ u32x4_t lora_row8(const uint16_t *src, int lim, int vec) {
+    if (vec && lim >= 8) return *reinterpret_cast<const u32x4_t *>(src);
+    return gather8(src, 1, lim);
 }
 
 // Epilogue: lane holds C[p .. p+3][m] for each (i, j, r4).  Writes either fp32 partials
@@ -769,6 +777,34 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = (float16_t){};
 
+    // Two register stages (steps v+1 and v+2 in flight) and two LDS stages (v and v+1), in the
+    // group's step numbering v.  Step v computes from LDS stage v & 1 while the other LDS stage
+    // receives step v+1 from register stage (v + 1) & 1, a quarter per MFMA k-substep; the
+    // register stage of v has been consumed, so it takes the global loads of v+2.  The loop
+    // body has no branches: prefetches past the range are issued anyway (in bounds of the
+    // operands or zero from the buffer range check, never consumed), so the compiler's wait
+    // counts only wait for the loads a store needs, never for the prefetch just issued.  An odd
+    // last step runs after the loop.  A group's step past the workgroup's range (KG > 1 only)
+    // reads its activations from an empty resource: zeros, so it adds nothing.  The loads of the
+    // first two steps are issued before the LoRA slab and the table barrier, so that their
+    // latency overlaps the slab's loads.
+    FwdWeight<DT, BP> wt[2] = {};
+    ActTile<BM, NT> at[2] = {};
+    const WeightRsrc wr = weight_rsrc(w);
+    const rsrc_t ar = act_rsrc<BM>(a, m0);
+    const rsrc_t ar0 = make_rsrc(a.act, 0);
+    const ActAddr aa = act_addr<NT>(a.ld_act);
+    const WAddr wa = fwd_waddr<BP>(wr, p0 - (wseg == 1 ? PH : 0), K);
+    auto stage = [&](int b, int64_t v) {
+        const int64_t st = s0 + g + KG * v;
+        at[b].load(KG > 1 && st >= s1 ? ar0 : ar, aa, static_cast<int>(st) * (BR * 2));
+        wt[b].load(wr, wa, st);
+    };
+    if (nv > 0) {
+        stage(0, 0);
+        stage(1, 1);
+    }
+
     // LoRA slab(s): acc = scale * B[p rows] . T[m rows]^T, before the weight product.
     const LoraDev &lo = a.lora[seg];
     if (!PAIR && lo.has && split == 0 && g == 0) {
@@ -779,14 +815,16 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
 #pragma unroll
             for (int i = 0; i < TP; ++i) {
                 const int64_t p = p0 + wp * (BP / WP) + i * 32 + r;
-                fa[i] = (p < w.rows && lim > 0) ? gather8(lo.b + p * lo.rank + k0 + kh, 1, lim)
-                                                : (u32x4_t){0u, 0u, 0u, 0u};
+                fa[i] = (p < w.rows && lim > 0)
+                            ? lora_row8(lo.b + p * lo.rank + k0 + kh, lim, lo.vec)
+                            : (u32x4_t){0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const int64_t m = m0 + wm * (BM / WM) + j * 32 + r;
-                fb[j] = (m < a.M && lim > 0) ? gather8(lo.t + m * lo.rank + k0 + kh, 1, lim)
-                                             : (u32x4_t){0u, 0u, 0u, 0u};
+                fb[j] = (m < a.M && lim > 0)
+                            ? lora_row8(lo.t + m * lo.rank + k0 + kh, lim, lo.vec)
+                            : (u32x4_t){0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int i = 0; i < TP; ++i)
@@ -799,33 +837,10 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
             for (int j = 0; j < TM; ++j) acc[i][j] *= lo.scale;
     }
 
-    // Two register stages (steps v+1 and v+2 in flight) and two LDS stages (v and v+1), in the
-    // group's step numbering v.  Step v computes from LDS stage v & 1 while the other LDS stage
-    // receives step v+1 from register stage (v + 1) & 1, a quarter per MFMA k-substep; the
-    // register stage of v has been consumed, so it takes the global loads of v+2.  The loop
-    // body has no branches: prefetches past the range are issued anyway (in bounds of the
-    // operands or zero from the buffer range check, never consumed), so the compiler's wait
-    // counts only wait for the loads a store needs, never for the prefetch just issued.  An odd
-    // last step runs after the loop.  A group's step past the workgroup's range (KG > 1 only)
-    // reads its activations from an empty resource: zeros, so it adds nothing.
-    FwdWeight<DT, BP> wt[2] = {};
-    ActTile<BM, NT> at[2] = {};
     __syncthreads();  // tables
-    const WeightRsrc wr = weight_rsrc(w);
-    const rsrc_t ar = act_rsrc<BM>(a, m0);
-    const rsrc_t ar0 = make_rsrc(a.act, 0);
-    const ActAddr aa = act_addr<NT>(a.ld_act);
-    const WAddr wa = fwd_waddr<BP>(wr, p0 - (wseg == 1 ? PH : 0), K);
-    auto stage = [&](int b, int64_t v) {
-        const int64_t st = s0 + g + KG * v;
-        at[b].load(KG > 1 && st >= s1 ? ar0 : ar, aa, static_cast<int>(st) * (BR * 2));
-        wt[b].load(wr, wa, st);
-    };
     uint8_t *sW[2] = {sT[g][0], sT[g][1]};
     uint8_t *sA[2] = {sT[g][0] + BP * ROWB, sT[g][1] + BP * ROWB};
     if (nv > 0) {
-        stage(0, 0);
-        stage(1, 1);
         at[0].store(sA[0]);
         {
             const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
@@ -1254,8 +1269,9 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
 #pragma unroll
                 for (int j = 0; j < TM; ++j) {
                     const int64_t m = m0 + wm * (BM / WM) + j * 32 + r;
-                    fb[j] = (m < a.M && lim > 0) ? gather8(lo.da + m * lo.rank + k0 + kh, 1, lim)
-                                                 : (u32x4_t){0u, 0u, 0u, 0u};
+                    fb[j] = (m < a.M && lim > 0)
+                                ? lora_row8(lo.da + m * lo.rank + k0 + kh, lim, lo.vec)
+                                : (u32x4_t){0u, 0u, 0u, 0u};
                 }
 #pragma unroll
                 for (int i = 0; i < TP; ++i)
@@ -1800,6 +1816,7 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
         d.rank = l.rank;
         d.scale = l.scale;
         d.has = 1;
+        d.vec = l.rank % 8 == 0 && aligned(l.t, 16) && aligned(l.b, 16);
     }
     if (m == 0 || n_out == 0) return NF4_OK;
     g.bias = static_cast<const uint16_t *>(bias);
@@ -1878,6 +1895,7 @@ extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, cons
         d.rank = l.rank;
         d.scale = l.scale;
         d.has = 1;
+        d.vec = l.rank % 8 == 0 && aligned(l.da, 16);
     }
     if (m == 0 || g.K == 0) return NF4_OK;
     g.out = dx;

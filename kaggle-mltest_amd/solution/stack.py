@@ -198,7 +198,8 @@ class ProjectionStack:
 
     def forward(self, ev=None, layers=None):
         """Queue the forward projections of every layer (or of `layers`).  `ev`: dict GEMM name
-        -> (start, end) events recorded around that GEMM's launch (one layer at a time)."""
+        -> (start, end) events recorded around that GEMM's launch (one layer at a time); GEMMs
+        not in it run unbracketed."""
         lib, dt, m = self.lib, self.dt, self.m
         s = torch.cuda.current_stream(self.dev).cuda_stream
         P = lambda t: t.data_ptr()  # noqa: E731
@@ -253,8 +254,9 @@ class ProjectionStack:
         self.backward(ev)
 
     def _timed(self, ev, name, fn):
-        if ev is not None:
+        timed = ev is not None and name in ev
+        if timed:
             ev[name][0].record()
         self._chk(fn(), name)
-        if ev is not None:
+        if timed:
             ev[name][1].record()
