@@ -175,6 +175,20 @@ __device__ __forceinline__ BlockTile block_tile(const GemmArgs &a, uint32_t b) {
                      static_cast<int>(__builtin_amdgcn_readfirstlane(r % sp)), a.splits};
 }
 
+// Logical workgroup of dispatched workgroup b of n.  The dispatcher deals workgroups to the 8
+// XCDs in turn (XCD b % 8), each XCD with its own L2; within every run of 256 consecutive
+// workgroups (one round of the 256 CUs) XCD x gets a contiguous range of logical tiles, so the
+// m tiles that share a weight tile (m fastest) run on one XCD and read it through one L2.
+// A bijection on every run of 256: rounds keep their tiles.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
+    constexpr uint32_t kXcds = 8, kRun = 256;
+    const uint32_t c0 = b & ~(kRun - 1);
+    const uint32_t len = n - c0 < kRun ? n - c0 : kRun;
+    const uint32_t j = b - c0, q = len / kXcds, r = len % kXcds;
+    const uint32_t x = j % kXcds, i = j / kXcds;
+    return __builtin_amdgcn_readfirstlane(c0 + (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i);
+}
+
 // The raw absmax inputs of block b, fetched with the packed bytes; rebuilt later by absmax_val.
 struct AbsIn {
     float s;      // absmax2 scale (nested) or the fp32 absmax
@@ -877,7 +891,8 @@ template <int DT, int BP, int BM, int WP, int WM, int EPI = 0, int KG = 1>
 __global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<BP, BM, KG>()];
     __shared__ float s_code2[EPI != 0 ? 2 : 1][256];
-    fwd_body<DT, BP, BM, WP, WM, EPI, KG>(a, a.map[0], blockIdx.x, lds, s_code2);
+    fwd_body<DT, BP, BM, WP, WM, EPI, KG>(a, a.map[0], xcd_tile(blockIdx.x, gridDim.x), lds,
+                                          s_code2);
 }
 
 // A two-part launch: workgroups [0, blocks0) run 256x256 tiles over the first part's map, the
@@ -889,10 +904,11 @@ __global__ __launch_bounds__(512) void fwd_head_tail_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
     __shared__ float s_code2[EPI != 0 ? 2 : 1][256];
     const uint32_t b0 = static_cast<uint32_t>(a.blocks0);
-    if (blockIdx.x < b0)
-        fwd_body<DT, 256, 256, 2, 4, EPI, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
+    const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
+    if (t < b0)
+        fwd_body<DT, 256, 256, 2, 4, EPI, 1>(a, a.map[0], t, lds, s_code2);
     else
-        fwd_body<DT, 128, 128, 2, 2, EPI, 2>(a, a.map[1], blockIdx.x - b0, lds, s_code2);
+        fwd_body<DT, 128, 128, 2, 2, EPI, 2>(a, a.map[1], t - b0, lds, s_code2);
 }
 
 // ------------------------------------------------------------------------ decode forward path
@@ -1356,7 +1372,7 @@ template <int DT, int BP, int BM, int WP, int WM, int KG = 1>
 __global__ __launch_bounds__(KG *WP *WM * 64) void dx_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<BP, BM, KG>()];
     __shared__ float s_code2[kMaxSeg][256];
-    dx_body<DT, BP, BM, WP, WM, KG>(a, a.map[0], blockIdx.x, lds, s_code2);
+    dx_body<DT, BP, BM, WP, WM, KG>(a, a.map[0], xcd_tile(blockIdx.x, gridDim.x), lds, s_code2);
 }
 
 // Two-part input-gradient launch (as fwd_head_tail_kernel): output columns of the first part
@@ -1366,10 +1382,11 @@ __global__ __launch_bounds__(512) void dx_head_tail_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
     __shared__ float s_code2[kMaxSeg][256];
     const uint32_t b0 = static_cast<uint32_t>(a.blocks0);
-    if (blockIdx.x < b0)
-        dx_body<DT, 256, 256, 2, 4, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
+    const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
+    if (t < b0)
+        dx_body<DT, 256, 256, 2, 4, 1>(a, a.map[0], t, lds, s_code2);
     else
-        dx_body<DT, 128, 128, 2, 2, 2>(a, a.map[1], blockIdx.x - b0, lds, s_code2);
+        dx_body<DT, 128, 128, 2, 2, 2>(a, a.map[1], t - b0, lds, s_code2);
 }
 
 // Split reduction over the tail columns [col0, col0 + n_out):
