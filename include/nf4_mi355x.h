@@ -42,6 +42,7 @@ extern "C" {
 #define NF4_F16 0
 #define NF4_BF16 1
 #define NF4_F32 2
+#define NF4_I32 3  /* int32 sums (nf4_int8_gemm output only) */
 
 /* One NF4 weight [rows, cols] (out_features x in_features) in bitsandbytes layout. */
 typedef struct nf4_weight {
@@ -219,6 +220,59 @@ int nf4_linear_swiglu_bwd(const void *x, int64_t m, int64_t ldx, const nf4_weigh
 int nf4_linear_swiglu_tiled(const void *x, int64_t m, int64_t ldx, const nf4_weight *gate_up,
                             void *out, int64_t ldo, const void *dh, int64_t lddh, int dtype,
                             void *stream, int backward, int tile);
+
+/* ------------------------------- int8 input gradients of the MLP (off the fp16 parity path) */
+/* The reference's T4 int8 backward (layer.py:299-442, 515-618, 992-1013): the input gradients
+ * of down and of gate|up as int8 GEMMs with one scale per token and one per weight column.
+ * Rounding to int8: ties away from zero, clamped to +-127 (layer.py:299-303).  Tolerance is the
+ * reference's own (test_kernels.py:323-357): int8 operands within 0.6 scale of their value,
+ * int8 products within 2e-2 of the largest fp32 result. */
+
+/* scale[c] = max(largest |W[:, c]| over the stacked rows, 1e-20) / 127, W dequantized and
+ * rounded to dtype (F16 / BF16): the fixed column scales of the transposed int8 weights.
+ * Replaces: _col_scales (layer.py:598-615). */
+size_t nf4_int8_colscale_workspace(const nf4_weight *ws, int nw);
+int nf4_int8_colscale(const nf4_weight *ws, int nw, float *scale, int dtype, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/* The stack as int8, transposed: q[c][r] = round(W[r][c] / scale[c]) with W the fp32 value
+ * code[nib] * absmax; q row-major [cols, sum rows] with rows ldq bytes apart.  Rows and cols of
+ * every weight multiples of 64.
+ * Replaces: nf4_int8_t_kernel / _int8_t (layer.py:338-369, 579-595). */
+int nf4_int8_weight_t(const nf4_weight *ws, int nw, const float *scale, int8_t *q, int64_t ldq,
+                      void *stream);
+
+/* The stack as int8 rows with one scale per row: s[r] = max(largest |W[r]|, 1e-20) / 127,
+ * q[r][c] = round(W[r][c] * (127 / largest)).
+ * Replaces: nf4_int8_rows_kernel / _int8_rows (layer.py:306-335, 565-576). */
+int nf4_int8_weight_rows(const nf4_weight *ws, int nw, int8_t *q, int64_t ldq, float *s,
+                         void *stream);
+
+/* One int8 row per activation row (dtype F16 / BF16 / F32, cols a multiple of 8): s[r] =
+ * max(largest |x[r]|, 1e-20) / 127, q[r][c] = round(x[r][c] * (127 / largest)).
+ * Replaces: row_quant_kernel / _row_quant (layer.py:372-382, 555-562). */
+int nf4_int8_rows(const void *x, int64_t rows, int64_t cols, int64_t ldx, int8_t *q, int64_t ldq,
+                  float *s, int dtype, void *stream);
+
+/* C[M, N] = A[M, K] . B[N, K]^T over int8 with exact int32 sums (K a multiple of 128, N of 4):
+ * out_dtype NF4_I32 writes the sums, F16 / BF16 writes round(fp32(C) * sa[m] * sb[n]).
+ * Workspace (int32 split-K partials): nf4_int8_gemm_workspace bytes.
+ * Replaces: torch._int_mm and the scaling of its result (layer.py:1003, 1010-1012;
+ *           test_kernels.py:348, 353). */
+size_t nf4_int8_gemm_workspace(int64_t m, int64_t n, int64_t k);
+int nf4_int8_gemm(const int8_t *a, int64_t m, int64_t lda, const int8_t *b, int64_t n,
+                  int64_t ldb, int64_t k, const float *sa, const float *sb, void *c, int64_t ldc,
+                  int out_dtype, void *workspace, size_t workspace_bytes, void *stream);
+
+/* SwiGLU backward on the int32 sums acc[M, I] of dh8 . Wd8^T with per-row int8 requantization:
+ * dh = fp32(acc) * sd[m] * cs[j]; with g, u the saved gate | up ([M, 2I], dtype) and
+ * sig = 1 / (1 + exp(-g)): q[m][j] = round(dh u sig (1 + g (1 - sig)) * 127 / peak),
+ * q[m][I + j] = round(dh g sig * 127 / peak), sq[m] = peak / 127, peak the row's largest
+ * |gradient| (at least 1e-20).
+ * Replaces: gate_up_act_bwd_i8_kernel (layer.py:414-442). */
+int nf4_int8_swiglu_bwd(const int32_t *acc, int64_t m, int64_t inter, int64_t ldacc,
+                        const float *sd, const float *cs, const void *gu, int64_t ldgu, int8_t *q,
+                        int64_t ldq, float *sq, int dtype, void *stream);
 
 /* ------------------------------------------- the projection's neighbours: RMSNorm, RoPE */
 

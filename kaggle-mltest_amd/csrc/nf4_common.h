@@ -97,6 +97,18 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     else return pack2_f16(a, b);
 }
 
+// One fp32 value rounded to nearest-even into fp16 / bf16 bits.  The empty asm keeps the fp32
+// value itself as the conversion's input: otherwise a product followed by the conversion can
+// be merged into one mixed-precision FMA (v_fma_mixlo_f16), which rounds the exact product once
+// instead of rounding the fp32 product, and differs where that fp32 product is an exact tie
+// between two fp16 values.
+template <int DT>
+__device__ __forceinline__ uint16_t round16(float v) {
+    asm volatile("" : "+v"(v));
+    if constexpr (DT == NF4_BF16) return __builtin_bit_cast(uint16_t, static_cast<bf16_t>(v));
+    else return __builtin_bit_cast(uint16_t, static_cast<half_t>(v));
+}
+
 // ---------------------------------------------------------- register-table NF4 lookup
 //
 // For one absmax s, the 16 possible dequantized values round(code[i] * s) (each the same single

@@ -45,10 +45,8 @@ template <int DT>
 __device__ __forceinline__ void store1(void *out, int64_t e, float v) {
     if constexpr (DT == NF4_F32) {
         static_cast<float *>(out)[e] = v;
-    } else if constexpr (DT == NF4_BF16) {
-        static_cast<bf16_t *>(out)[e] = static_cast<bf16_t>(v);
     } else {
-        static_cast<half_t *>(out)[e] = static_cast<half_t>(v);
+        static_cast<uint16_t *>(out)[e] = round16<DT>(v);
     }
 }
 

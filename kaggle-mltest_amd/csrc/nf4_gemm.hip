@@ -130,8 +130,7 @@ __device__ __forceinline__ float to_f32(uint16_t v) {
 
 template <int DT>
 __device__ __forceinline__ uint16_t from_f32(float v) {
-    if constexpr (DT == NF4_BF16) return __builtin_bit_cast(uint16_t, static_cast<bf16_t>(v));
-    else return __builtin_bit_cast(uint16_t, static_cast<half_t>(v));
+    return round16<DT>(v);
 }
 
 __device__ __forceinline__ int seg_of_tile(const GemmArgs &a, const TileMap &tm, int64_t t) {

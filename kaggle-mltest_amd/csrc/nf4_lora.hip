@@ -18,8 +18,7 @@ __device__ __forceinline__ float ld1(const uint16_t *p) {
 
 template <int DT>
 __device__ __forceinline__ uint16_t st1(float v) {
-    if constexpr (DT == NF4_BF16) return __builtin_bit_cast(uint16_t, static_cast<bf16_t>(v));
-    else return __builtin_bit_cast(uint16_t, static_cast<half_t>(v));
+    return round16<DT>(v);
 }
 
 template <int DT>

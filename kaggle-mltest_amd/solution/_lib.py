@@ -16,7 +16,7 @@ import torch
 LIB_PATH = Path(__file__).with_name("libnf4_mi355x.so")
 
 NF4_OK, NF4_ERR_ARG, NF4_ERR_UNSUPPORTED, NF4_ERR_LAUNCH, NF4_ERR_WORKSPACE = range(5)
-NF4_F16, NF4_BF16, NF4_F32 = 0, 1, 2
+NF4_F16, NF4_BF16, NF4_F32, NF4_I32 = 0, 1, 2, 3
 NF4_MAX_SEGMENTS = 8
 
 DTYPE_CODE = {torch.float16: NF4_F16, torch.bfloat16: NF4_BF16, torch.float32: NF4_F32}
@@ -102,6 +102,22 @@ _SIGNATURES = {
     "nf4_swiglu_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
                                c_void_p, c_int64, c_int64, c_int, c_void_p]),
     "nf4_bias_grad": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p]),
+    "nf4_int8_colscale_workspace": (c_size_t, [ctypes.POINTER(NF4Weight), c_int]),
+    "nf4_int8_colscale": (c_int, [ctypes.POINTER(NF4Weight), c_int, c_void_p, c_int, c_void_p,
+                                  c_size_t, c_void_p]),
+    "nf4_int8_weight_t": (c_int, [ctypes.POINTER(NF4Weight), c_int, c_void_p, c_void_p, c_int64,
+                                  c_void_p]),
+    "nf4_int8_weight_rows": (c_int, [ctypes.POINTER(NF4Weight), c_int, c_void_p, c_int64,
+                                     c_void_p, c_void_p]),
+    "nf4_int8_rows": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
+                              c_int, c_void_p]),
+    "nf4_int8_gemm_workspace": (c_size_t, [c_int64, c_int64, c_int64]),
+    "nf4_int8_gemm": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64,
+                              c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_size_t,
+                              c_void_p]),
+    "nf4_int8_swiglu_bwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                    c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int,
+                                    c_void_p]),
     "nf4_add_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_float, c_float, c_void_p, c_void_p, c_int64, c_int64,
                                 c_float, c_int, c_void_p]),

@@ -1,0 +1,67 @@
+"""int8 input gradients of the SwiGLU MLP on gfx950 int8 MFMA: the reference's T4 int8 backward
+(/root/reference/solution/layer.py:515-618, 992-1013), kept off the fp16 parity path and held to
+the reference's own int8 tolerance (test_kernels.py:323-357).
+
+    dh2 [n, H]  -> int8 rows dh8, sdh                       (row_quant, layer.py:555-562)
+    acc = dh8 . Wd8^T        int32 [n, I]                   (layer.py:1003)
+          Wd8 = W_down transposed to int8 with the fixed column scales cs_d
+    q8, sq = SwiGLU backward of acc * sdh * cs_d on the saved gate | up, int8 per row
+                                                            (gate_up_act_bwd_i8_kernel)
+    dy2 = fp32(q8 . Wgu8^T) * sq * cs_gu  -> GEMM dtype     (layer.py:1008-1012)
+
+Column scales are computed once per MLP (the reference caches them per module for the run,
+layer.py:598-615); the int8 weights are made from the NF4 bytes at each use, as the fp16 ones
+are.  The reference splits the first GEMM into 512-token chunks to bound a 15 GB GPU's memory;
+one launch covers every token here."""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+
+INT8 = True           # int8 input gradients of the MLP (the reference's default)
+INT8_FORWARD = False  # the forward stays fp16 (layer.py:533)
+
+
+def int8_eligible(hidden: int, inter: int, blocksize: int) -> bool:
+    """Shapes the int8 kernels tile exactly (layer.py:538-548)."""
+    return hidden % 128 == 0 and inter % 128 == 0 and 128 % blocksize == 0
+
+
+class ColumnScales:
+    """Per-MLP cache of (cs_gu, cs_d), keyed by the packed weight tensors."""
+
+    def __init__(self):
+        self._cache = {}
+
+    def get(self, gate, up, down, dtype=torch.float16):
+        key = (gate[0].data_ptr(), up[0].data_ptr(), down[0].data_ptr(), dtype)
+        hit = self._cache.get(key)
+        if hit is None:
+            hit = (kernels.int8_colscale([gate, up], dtype), kernels.int8_colscale([down], dtype))
+            self._cache[key] = hit
+        return hit
+
+
+def mlp_input_grad_int8(dh2: torch.Tensor, gu: torch.Tensor, gate, up, down,
+                        scales: tuple | None = None, dtype=None) -> torch.Tensor:
+    """dy2 [n, H] = d(down(silu(g) u)) / dx for the gradient dh2 [n, H] at the MLP output, the
+    saved gate | up product gu [n, 2I] and the NF4 weights (packed, quant_state), through two
+    int8 GEMMs.  `scales`: (cs_gu, cs_d) from ColumnScales (computed here when None)."""
+    dtype = dtype or gu.dtype
+    inter = int(gate[1].shape[0])
+    hidden = int(gate[1].shape[1])
+    if not int8_eligible(hidden, inter, int(gate[1].blocksize)):
+        raise ValueError(f"int8 input gradients need hidden and inter multiples of 128 "
+                         f"(got {hidden}, {inter}) and a block size dividing 128")
+    cs_gu, cs_d = scales if scales is not None else (kernels.int8_colscale([gate, up], dtype),
+                                                      kernels.int8_colscale([down], dtype))
+    dh8, sdh = kernels.int8_rows(dh2)
+    acc = kernels.int8_gemm(dh8, kernels.int8_weight_t([down], cs_d))
+    q8, sq = kernels.int8_swiglu_bwd(acc, sdh, cs_d, gu)
+    return kernels.int8_gemm(q8, kernels.int8_weight_t([gate, up], cs_gu), sq, cs_gu,
+                             out_dtype=dtype)
+
+
+__all__ = ["INT8", "INT8_FORWARD", "int8_eligible", "ColumnScales", "mlp_input_grad_int8"]

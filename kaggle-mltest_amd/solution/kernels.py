@@ -405,3 +405,96 @@ def lora_wgrad_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor
     check(lib.nf4_lora_wgrad_multi(arr, n, m, rank, _code(dtype),
                                    ws.data_ptr() if ws is not None else None, nbytes,
                                    stream_of(stream_tensor)), "nf4_lora_wgrad_multi")
+
+
+# ------------------------------------------------- int8 input gradients (off the parity path)
+
+def int8_colscale(weights, dtype=torch.float16) -> torch.Tensor:
+    """fp32 [cols]: max(largest |W[:, c]|, 1e-20) / 127 over the stacked weights, W rounded to
+    `dtype` (the fixed column scales of the transposed int8 weights)."""
+    arr = _descs(weights)
+    lib = load()
+    dev = weights[0][0].device
+    cols = int(weights[0][1].shape[1])
+    out = torch.empty(cols, dtype=torch.float32, device=dev)
+    nb = lib.nf4_int8_colscale_workspace(arr, len(weights))
+    ws = _workspace(nb, dev)
+    check(lib.nf4_int8_colscale(arr, len(weights), out.data_ptr(), _code(dtype),
+                                ws.data_ptr() if ws is not None else None, nb, stream_of(out)),
+          "nf4_int8_colscale")
+    return out
+
+
+def int8_weight_t(weights, scale: torch.Tensor) -> torch.Tensor:
+    """int8 [cols, sum rows]: the stacked weights transposed, divided by the column scales."""
+    arr = _descs(weights)
+    rows = sum(int(qs.shape[0]) for _, qs in weights)
+    cols = int(weights[0][1].shape[1])
+    q = torch.empty((cols, rows), dtype=torch.int8, device=scale.device)
+    check(load().nf4_int8_weight_t(arr, len(weights), scale.data_ptr(), q.data_ptr(), rows,
+                                   stream_of(q)), "nf4_int8_weight_t")
+    return q
+
+
+def int8_weight_rows(weights):
+    """(int8 [sum rows, cols], fp32 [sum rows]): the stacked weights with one scale per row."""
+    arr = _descs(weights)
+    rows = sum(int(qs.shape[0]) for _, qs in weights)
+    cols = int(weights[0][1].shape[1])
+    dev = weights[0][0].device
+    q = torch.empty((rows, cols), dtype=torch.int8, device=dev)
+    s = torch.empty(rows, dtype=torch.float32, device=dev)
+    check(load().nf4_int8_weight_rows(arr, len(weights), q.data_ptr(), cols, s.data_ptr(),
+                                      stream_of(q)), "nf4_int8_weight_rows")
+    return q, s
+
+
+def int8_rows(x: torch.Tensor):
+    """(int8 [M, N], fp32 [M]): one int8 row per row of x with scale largest |x| / 127."""
+    _check_device(x)
+    m, n = x.shape
+    q = torch.empty((m, n), dtype=torch.int8, device=x.device)
+    s = torch.empty(m, dtype=torch.float32, device=x.device)
+    code = _code(x.dtype, (torch.float16, torch.bfloat16, torch.float32))
+    check(load().nf4_int8_rows(x.data_ptr() if m else None, m, n, x.stride(0), q.data_ptr(), n,
+                               s.data_ptr(), code, stream_of(x)), "nf4_int8_rows")
+    return q, s
+
+
+def int8_gemm(a: torch.Tensor, b: torch.Tensor, sa: torch.Tensor | None = None,
+              sb: torch.Tensor | None = None, out_dtype=None) -> torch.Tensor:
+    """a [M, K] . b [N, K]^T over int8: int32 sums (out_dtype None) or
+    round(fp32(C) * sa[m] * sb[n]) in out_dtype (float16 / bfloat16)."""
+    _check_device(a, b)
+    m, k = a.shape
+    n = b.shape[0]
+    lib = load()
+    if out_dtype is None:
+        out = torch.empty((m, n), dtype=torch.int32, device=a.device)
+        code = _lib.NF4_I32
+    else:
+        out = torch.empty((m, n), dtype=out_dtype, device=a.device)
+        code = _code(out_dtype)
+    nb = lib.nf4_int8_gemm_workspace(m, n, k)
+    ws = _workspace(nb, a.device)
+    check(lib.nf4_int8_gemm(a.data_ptr(), m, a.stride(0), b.data_ptr(), n, b.stride(0), k,
+                            sa.data_ptr() if sa is not None else None,
+                            sb.data_ptr() if sb is not None else None, out.data_ptr(),
+                            out.stride(0), code, ws.data_ptr() if ws is not None else None, nb,
+                            stream_of(a)), "nf4_int8_gemm")
+    return out
+
+
+def int8_swiglu_bwd(acc: torch.Tensor, sd: torch.Tensor, cs: torch.Tensor,
+                    gu: torch.Tensor):
+    """(int8 [M, 2I], fp32 [M]): SwiGLU backward of the int32 sums acc [M, I] (scaled by
+    sd[m] cs[j]) with the saved gate | up [M, 2I], requantized with one scale per row."""
+    _check_device(acc, sd, cs, gu)
+    m, inter = acc.shape
+    q = torch.empty((m, 2 * inter), dtype=torch.int8, device=acc.device)
+    sq = torch.empty(m, dtype=torch.float32, device=acc.device)
+    check(load().nf4_int8_swiglu_bwd(acc.data_ptr(), m, inter, acc.stride(0), sd.data_ptr(),
+                                     cs.data_ptr(), gu.data_ptr(), gu.stride(0), q.data_ptr(),
+                                     2 * inter, sq.data_ptr(), _code(gu.dtype), stream_of(acc)),
+          "nf4_int8_swiglu_bwd")
+    return q, sq

@@ -409,6 +409,116 @@ def qkv_rope_bwd(dq, dk, dv, cos, sin, n_kv):
     return torch.cat((back(dq).reshape(t, -1), back(gk).reshape(t, -1), gv.reshape(t, -1)), 1)
 
 
+# ----------------------------------------------------------------- int8 input gradients
+#
+# The reference's int8 MLP backward (layer.py:299-442, 515-618, 992-1013), restated in numpy
+# float32 with every product / quotient rounded on its own; integer GEMMs in int64 (exact).
+
+def round_i8(v: np.ndarray) -> np.ndarray:
+    """Ties away from zero, clamped to [-127, 127] (layer.py:299-303):
+    ``floor(v + 0.5)`` for v >= 0, ``-floor(0.5 - v)`` otherwise, in fp32."""
+    v = np.asarray(v, dtype=np.float32)
+    half = np.float32(0.5)
+    r = np.where(v >= 0, np.floor(v + half), -np.floor(half - v)).astype(np.float32)
+    return np.clip(r, -127, 127).astype(np.int8)
+
+
+def int8_rows(x) -> tuple[np.ndarray, np.ndarray]:
+    """One int8 row per row (row_quant_kernel, layer.py:372-382): top = max(max|x|, 1e-20),
+    q = round(x * fp32(127 / top)), s = fp32(top / 127)."""
+    x = _np32(x)
+    top = np.maximum(np.abs(x).max(axis=1), np.float32(1e-20)).astype(np.float32)
+    inv = (np.float32(127.0) / top).astype(np.float32)
+    q = round_i8((x * inv[:, None]).astype(np.float32))
+    return q, (top / np.float32(127.0)).astype(np.float32)
+
+
+def _np32(x) -> np.ndarray:
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().float().numpy()
+    return np.asarray(x, dtype=np.float32)
+
+
+def stack_f32(weights) -> np.ndarray:
+    """fp32 products code[nib] * absmax of stacked weights [(packed, OracleQuantState)]."""
+    return np.concatenate([dequantize_f32(p, st).reshape(st.shape) for p, st in weights])
+
+
+def col_scales(weights, dtype: str = "f16") -> np.ndarray:
+    """Per input column, max(largest |W|, 1e-20) / 127 with W dequantized to ``dtype``
+    (_col_scales, layer.py:598-615)."""
+    w = np.concatenate([_as_f32(dequantize(p, st, dtype), dtype).reshape(st.shape)
+                        for p, st in weights])
+    top = np.abs(w).max(axis=0).astype(np.float32)
+    return (np.maximum(top, np.float32(1e-20)) / np.float32(127.0)).astype(np.float32)
+
+
+def _as_f32(w: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return (w.astype(np.uint32) << 16).view(np.float32)
+    return w.astype(np.float32)
+
+
+def int8_weight_t(weights, scale: np.ndarray) -> np.ndarray:
+    """The stack as int8, transposed: q[c][r] = round(fp32(W[r][c] / scale[c])) with W the fp32
+    product (nf4_int8_t_kernel, layer.py:338-369)."""
+    w = stack_f32(weights)
+    return np.ascontiguousarray(round_i8((w / scale[None, :]).astype(np.float32)).T)
+
+
+def int8_weight_rows(weights) -> tuple[np.ndarray, np.ndarray]:
+    """The stack as int8 rows with one scale per row (nf4_int8_rows_kernel, layer.py:306-335)."""
+    return int8_rows(stack_f32(weights))
+
+
+def int8_matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Exact ``a [M, K] . b [N, K]^T`` of int8 operands (torch._int_mm), as int64: evaluated in
+    float64, which holds every partial sum exactly (|sum| <= 127^2 K < 2^53 for K < 5e8)."""
+    assert a.shape[1] * 127 * 127 < 2 ** 53
+    return (a.astype(np.float64) @ b.astype(np.float64).T).astype(np.int64)
+
+
+def int8_scale(acc: np.ndarray, sa: np.ndarray, sb: np.ndarray) -> np.ndarray:
+    """fp32(acc) * sa[m] * sb[n], left to right (layer.py:1012)."""
+    f = acc.astype(np.float32)
+    return ((f * sa[:, None].astype(np.float32)).astype(np.float32) *
+            sb[None, :].astype(np.float32)).astype(np.float32)
+
+
+def int8_swiglu_bwd(acc: np.ndarray, sd: np.ndarray, cs: np.ndarray, gu) -> tuple:
+    """gate_up_act_bwd_i8_kernel (layer.py:414-442): dh = fp32(acc) * sd[m] * cs[j]; with g, u
+    the saved gate | up halves and sig = 1 / (1 + exp(-g)): d_gate = dh u sig (1 + g (1 - sig)),
+    d_up = dh g sig; q = round(grad * fp32(127 / peak)) per row over both halves (peak = max(
+    largest |grad|, 1e-20)), sq = peak / 127.  Returns (q [M, 2I] int8, sq, d_gate, d_up)."""
+    gu = _np32(gu)
+    inter = acc.shape[1]
+    g, u = gu[:, :inter], gu[:, inter:]
+    f32 = np.float32
+    dh = ((acc.astype(f32) * sd[:, None].astype(f32)).astype(f32) * cs[None, :].astype(f32)).astype(f32)
+    sig = (f32(1.0) / (f32(1.0) + np.exp(-g).astype(f32))).astype(f32)
+    du = ((dh * g).astype(f32) * sig).astype(f32)
+    dg = (((dh * u).astype(f32) * sig).astype(f32) *
+          (f32(1.0) + (g * (f32(1.0) - sig)).astype(f32)).astype(f32)).astype(f32)
+    peak = np.maximum(np.maximum(np.abs(dg).max(axis=1), np.abs(du).max(axis=1)), f32(1e-20))
+    peak = peak.astype(f32)
+    inv = (f32(127.0) / peak).astype(f32)
+    q = np.concatenate([round_i8((dg * inv[:, None]).astype(f32)),
+                        round_i8((du * inv[:, None]).astype(f32))], axis=1)
+    return q, (peak / f32(127.0)).astype(f32), dg, du
+
+
+def mlp_dx_int8(dh2, gu, gate_up, down, dtype: str = "f16"):
+    """The int8 MLP input gradient (layer.py:992-1013, without the 512-token chunking, which
+    only bounds the T4's memory): dh2 -> int8 rows, . int8 W_down^T (column scales), SwiGLU
+    backward requantized, . int8 W_gate|up^T, scaled.  Returns fp32 dy2 before the rounding
+    to the GEMM dtype."""
+    cs_gu, cs_d = col_scales(gate_up, dtype), col_scales(down, dtype)
+    dh8, sdh = int8_rows(dh2)
+    acc = int8_matmul(dh8, int8_weight_t(down, cs_d))
+    q8, sq, _, _ = int8_swiglu_bwd(acc, sdh, cs_d, gu)
+    return int8_scale(int8_matmul(q8, int8_weight_t(gate_up, cs_gu)), sq, cs_gu)
+
+
 def rel_errors(out, ref) -> tuple[float, float]:
     """(max |out-ref| / max |ref|, mean |out-ref| / mean |ref|): the reference's ``_rel``
     (layer.py:1253-1254) and its mean counterpart."""

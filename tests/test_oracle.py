@@ -270,3 +270,103 @@ def test_qkv_rope_bwd_matches_autograd():
     q, k, v, _, _ = o.qkv_rope(qa, cos, sin, 6, 2, 8)
     ((q * gq).sum() + (k * gk).sum() + (v * gv).sum()).backward()
     torch.testing.assert_close(o.qkv_rope_bwd(gq, gk, gv, cos, sin, 2), qa.grad)
+
+
+# ------------------------------------------------------------------ int8 input gradients
+
+def test_round_i8_known_answers():
+    """Ties away from zero and the clamp (layer.py:299-303), evaluated in fp32: v + 0.5 rounds
+    in fp32 before the floor, so the largest float below 0.5 goes to 1 as it does there."""
+    v = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 0.49, -0.49, 126.5, 127.6, -300.0, 0.0,
+                  np.nextafter(np.float32(0.5), np.float32(0))], dtype=np.float32)
+    assert o.round_i8(v).tolist() == [1, 2, 3, -1, -2, -3, 0, 0, 127, 127, -127, 0, 1]
+
+
+def _i8_weights(seed, shapes, nested=True):
+    g = np.random.default_rng(seed)
+    return [o.quantize_nf4(g.standard_normal((r, c)).astype(np.float32) * 0.02,
+                           compress_statistics=nested) for r, c in shapes]
+
+
+def test_int8_rows_invariants():
+    """Each row's largest |x| maps to +-127, every value lies within half a step of q * s, and
+    s = largest / 127."""
+    g = np.random.default_rng(7)
+    x = (g.standard_normal((20, 96)) * np.logspace(-3, 2, 20)[:, None]).astype(np.float32)
+    q, s = o.int8_rows(x)
+    top = np.abs(x).max(axis=1)
+    assert np.array_equal(s, (top / np.float32(127)).astype(np.float32))
+    assert np.array_equal(np.abs(q[np.arange(20), np.abs(x).argmax(axis=1)]), np.full(20, 127))
+    assert np.all(np.abs(q.astype(np.float64) * s[:, None] - x) <= 0.5 * s[:, None] * (1 + 1e-5))
+    q0, s0 = o.int8_rows(np.zeros((2, 8), np.float32))  # empty rows: scale 1e-20 / 127
+    assert not q0.any() and np.all(s0 > 0)
+
+
+def test_int8_matmul_is_exact():
+    g = np.random.default_rng(8)
+    a = g.integers(-127, 128, (5, 7), dtype=np.int8)
+    b = g.integers(-127, 128, (3, 7), dtype=np.int8)
+    ref = [[sum(int(a[i, k]) * int(b[j, k]) for k in range(7)) for j in range(3)] for i in range(5)]
+    assert o.int8_matmul(a, b).tolist() == ref
+    big = np.full((1, 17920), 127, np.int8)
+    assert int(o.int8_matmul(big, big)[0, 0]) == 127 * 127 * 17920  # fits int32
+
+
+def test_int8_col_scales_and_weights():
+    """Column scales from the dtype-rounded weights (torch's amax over the fp16 / bf16
+    dequantized stack, an independent route), and the transposed int8 stack within half a
+    step of the fp32 weights (the reference test's 0.6 scale bound, test_kernels.py:344-346)."""
+    ws = _i8_weights(9, [(128, 192), (64, 192)])
+    for dt in ("f16", "bf16"):
+        w = torch.cat([torch.from_numpy(o.dequantize(p, st, dt).view(np.int16)).view(
+            torch.bfloat16 if dt == "bf16" else torch.float16).float() for p, st in ws])
+        ref = (w.abs().amax(0).clamp_min(1e-20) / 127).numpy()
+        assert np.array_equal(o.col_scales(ws, dt), ref.astype(np.float32))
+    cs = o.col_scales(ws)
+    qt = o.int8_weight_t(ws, cs)
+    wf = o.stack_f32(ws)
+    assert qt.shape == (192, 192) and qt.dtype == np.int8
+    assert np.all(np.abs(qt.T.astype(np.float64) * cs[None, :] - wf) <= 0.5 * cs[None, :] * 1.01)
+    q, s = o.int8_weight_rows(ws)
+    assert np.all(np.abs(q.astype(np.float64) * s[:, None] - wf) <= 0.5 * s[:, None] * 1.01)
+
+
+def test_int8_swiglu_bwd_against_float64():
+    """The SwiGLU gradients before requantization agree with a float64 evaluation of the same
+    formula, and the int8 codes reproduce them within half a step."""
+    g = np.random.default_rng(10)
+    m, inter = 6, 40
+    acc = g.integers(-40000, 40000, (m, inter)).astype(np.int64)
+    sd = (g.random(m) * 1e-3 + 1e-4).astype(np.float32)
+    cs = (g.random(inter) * 1e-3 + 1e-4).astype(np.float32)
+    gu = (g.standard_normal((m, 2 * inter)) * 2).astype(np.float16).astype(np.float32)
+    q, sq, dg, du = o.int8_swiglu_bwd(acc, sd, cs, gu)
+    d = acc.astype(np.float64) * sd[:, None] * cs[None, :]
+    gg, uu = gu[:, :inter].astype(np.float64), gu[:, inter:].astype(np.float64)
+    sig = 1 / (1 + np.exp(-gg))
+    np.testing.assert_allclose(dg, d * uu * sig * (1 + gg * (1 - sig)), rtol=2e-5, atol=1e-12)
+    np.testing.assert_allclose(du, d * gg * sig, rtol=2e-5, atol=1e-12)
+    both = np.concatenate([dg, du], axis=1)
+    assert np.all(np.abs(q.astype(np.float64) * sq[:, None] - both) <= 0.5 * sq[:, None] * 1.01)
+    assert np.array_equal(np.abs(q).max(axis=1), np.full(m, 127))
+
+
+def test_int8_mlp_dx_against_fp32():
+    """The composite int8 MLP input gradient against the fp32 one on the same dequantized
+    weights: within 3e-2 of the largest |dy2| (two int8 products, each held to 2e-2 by the
+    reference's own test, test_kernels.py:350, 357)."""
+    g = np.random.default_rng(11)
+    n, hidden, inter = 96, 256, 384
+    gate, up = _i8_weights(12, [(inter, hidden), (inter, hidden)])
+    down = _i8_weights(13, [(hidden, inter)])[0]
+    x = torch.from_numpy(g.standard_normal((n, hidden)).astype(np.float32)).half()
+    wg, wu, wd = (torch.from_numpy(o.dequantize(p, st)).float() for p, st in (gate, up, down))
+    gu = torch.cat([x.float() @ wg.t(), x.float() @ wu.t()], 1).half()
+    dh2 = torch.from_numpy(g.standard_normal((n, hidden)).astype(np.float32) * 1e-2)
+    dy2 = o.mlp_dx_int8(dh2, gu, [gate, up], [down])
+    gg, uu = gu.float()[:, :inter], gu.float()[:, inter:]
+    sig = torch.sigmoid(gg)
+    dact = dh2 @ wd
+    ref = torch.cat([dact * uu * sig * (1 + gg * (1 - sig)), dact * gg * sig], 1) @ torch.cat([wg, wu])
+    err = np.abs(dy2 - ref.numpy()).max() / np.abs(ref.numpy()).max()
+    assert err <= 3e-2, err
