@@ -56,6 +56,45 @@ def test_reference_shapes_bit_exact(cuda, shape):
     assert torch.equal(_bits(out), _oracle(packed, qs, "f16"))
 
 
+def _double_rounding_pairs(count, seed=0):
+    """(code index, fp32 absmax) pairs whose fp32 product code * absmax is an exact fp16 tie
+    while the exact product is not: rounding the fp32 product (the element formula's two
+    roundings) and rounding the exact product once give neighbouring fp16 values."""
+    code = o.NF4_CODE.astype(np.float32)
+    rng = np.random.default_rng(seed)
+    a = rng.uniform(1e-3, 1e-1, 2_000_000).astype(np.float32)
+    i = rng.integers(0, 16, a.size)
+    double = (code[i] * a).astype(np.float32).astype(np.float16)
+    single = (code[i].astype(np.float64) * a.astype(np.float64)).astype(np.float16)
+    hit = np.nonzero(double != single)[0]  # ~3.5e-5 of the draws
+    assert hit.size >= 16
+    hit = np.resize(hit, count)
+    return i[hit], a[hit]
+
+
+@pytest.mark.parametrize("shape,bs", [((4, 30), 2), ((3, 66), 64)])
+def test_scalar_paths_round_the_fp32_product(cuda, shape, bs):
+    """The scalar dequant paths (element kernel for blocksize 2; the ragged tail of the 8-element
+    kernel) on products where one rounding of the exact product would differ from rounding the
+    fp32 product: the output must be the latter, bit for bit."""
+    banner("dequant scalar double rounding", shape, bs)
+    n = shape[0] * shape[1]
+    nb = -(-n // bs)
+    idx, am = _double_rounding_pairs(nb)
+    nib = np.repeat(idx, bs)[:n].astype(np.uint8)
+    if n % 2:
+        nib = np.append(nib, 0)
+    packed = ((nib[0::2] << 4) | nib[1::2]).astype(np.uint8)
+    st = o.OracleQuantState(absmax=am.astype(np.float32), shape=shape, code=o.NF4_CODE.copy(),
+                            blocksize=bs)
+    p, qs = to_device_state(packed, st, cuda)
+    from solution import kernels
+
+    out = kernels.dequant([(p, qs)], torch.float16)
+    ref = o.dequantize(packed, st, "f16")
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("nested", [True, False])
 @pytest.mark.parametrize("shape,bs", [((7, 9), 64), ((33, 64), 32), ((100, 384), 128),
