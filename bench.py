@@ -65,6 +65,8 @@ def parse():
                     help="skip the small-M forward sweeps over the 28-layer stacks")
     ap.add_argument("--no-swiglu", action="store_true",
                     help="skip the gate|up + SwiGLU epilogue comparison")
+    ap.add_argument("--no-int8", action="store_true",
+                    help="skip the int8 MLP input-gradient leg (the reference's T4 backward)")
     ap.add_argument("--no-norm-rope", action="store_true",
                     help="skip the RMSNorm / RoPE neighbours of the projection")
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -197,6 +199,72 @@ def swiglu_leg(dtype, dev, reps=20, warmup=3):
         "fused_fwd_tflops": round(gflop / res["fused_fwd"] * 1e3, 1),
         "speedup_fwd": round(res["unfused_fwd"] / res["fused_fwd"], 3),
         "speedup_bwd": round(res["unfused_bwd"] / res["fused_bwd"], 3)}}
+
+
+# ---------------------------------------------- int8 input gradients (off the parity path)
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def int8_leg(dev, reps=20):
+    """The MLP input gradient at M=2048 on the Qwen2.5-1.5B shapes (dh2 [M, 1536] -> dy2) two
+    ways, each captured in a HIP graph: the fp16 path (fused NF4 dX GEMM of down, SwiGLU
+    backward, fused NF4 dX GEMM of gate|up) and the int8 path of the reference's T4 backward
+    (int8 rows, int8 weights made from the NF4 bytes, two int8 GEMMs, SwiGLU backward
+    requantized); plus each int8 GEMM alone against the 5.0 POP/s dense int8 peak."""
+    import torch
+
+    from solution import kernels
+    from solution.int8_mlp import ColumnScales, mlp_input_grad_int8
+    from solution.quant_state import quantize_4bit
+
+    hidden, inter = 1536, 8960
+    g = torch.Generator(device=dev)
+    w = []
+    for s, shape in ((401, (inter, hidden)), (402, (inter, hidden)), (403, (hidden, inter))):
+        g.manual_seed(s)
+        packed, qs = quantize_4bit(torch.randn(*shape, generator=g, device=dev) * 0.02)
+        w.append((packed.view(-1), qs))
+    gate, up, down = w
+    g.manual_seed(404)
+    x = torch.randn(M, hidden, generator=g, device=dev).half()
+    dh2 = (torch.randn(M, hidden, generator=g, device=dev) * 1e-2).half()
+    gu = kernels.linear_fwd(x, [gate, up])
+    d_act = torch.empty(M, inter, dtype=torch.float16, device=dev)
+    dgu = torch.empty(M, 2 * inter, dtype=torch.float16, device=dev)
+    dy = torch.empty(M, hidden, dtype=torch.float16, device=dev)
+
+    def fp16_path():
+        kernels.linear_dx(dh2, [down], out=d_act)
+        kernels.swiglu_bwd(d_act, gu[:, :inter], gu[:, inter:], dgu[:, :inter], dgu[:, inter:])
+        kernels.linear_dx(dgu, [gate, up], out=dy)
+
+    scales = ColumnScales().get(gate, up, down)
+    cs_gu, cs_d = scales
+    dh8, sdh = kernels.int8_rows(dh2)
+    wd8 = kernels.int8_weight_t([down], cs_d)
+    acc = kernels.int8_gemm(dh8, wd8)
+    q8, sq = kernels.int8_swiglu_bwd(acc, sdh, cs_d, gu)
+    wgu8 = kernels.int8_weight_t([gate, up], cs_gu)
+    t = {"fp16_path": _time_graph(torch, fp16_path, reps),
+         "int8_path": _time_graph(torch, lambda: mlp_input_grad_int8(dh2, gu, gate, up, down,
+                                                                       scales), reps),
+         "int8_gemm_down": _time_graph(torch, lambda: kernels.int8_gemm(dh8, wd8), reps),
+         "int8_gemm_gate_up": _time_graph(torch, lambda: kernels.int8_gemm(
+             q8, wgu8, sq, cs_gu, out_dtype=torch.float16), reps),
+         "int8_weights": _time_graph(torch, lambda: (kernels.int8_weight_t([down], cs_d),
+                                                     kernels.int8_weight_t([gate, up], cs_gu)),
+                                     reps)}
+    ops = 2 * M * inter * hidden
+    tops = {n: round(ops / (t[n] * 1e-3) / 1e12, 1) for n in ("int8_gemm_down", "int8_gemm_gate_up")}
+    return {"int8_mlp_dx": {
+        "workload": "Qwen2.5-1.5B MLP input gradient (down 1536x8960, gate|up 2x8960x1536), "
+                    "M=2048, HIP graph replay; int8 = the reference's T4 int8 backward "
+                    "(off the fp16 parity path, its own tolerance)",
+        "us": {n: round(v * 1e3, 2) for n, v in t.items()},
+        "speedup_int8_vs_fp16": round(t["fp16_path"] / t["int8_path"], 3),
+        "int8_gemm_tops": tops, "peak_int8_tops": PEAK_INT8_TOPS,
+        "int8_gemm_frac": {n: round(v / PEAK_INT8_TOPS, 4) for n, v in tops.items()}}}
 
 
 # ------------------------------------------------- the projection's neighbours (norm, RoPE)
@@ -594,6 +662,8 @@ def main():
                                             "frac": dq["frac"], "traffic": None})
     if not args.no_swiglu:
         out.update(swiglu_leg(dtype, dev))
+    if not args.no_int8 and args.dtype == "f16":
+        out.update(int8_leg(dev))
     if not args.no_norm_rope:
         out.update(norm_rope_leg(dtype, dev))
     if not args.no_stack:
