@@ -272,73 +272,78 @@ struct I8Args {
 
 __device__ __forceinline__ int i8swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 
-struct I8Tile {  // 128 rows x 128 bytes, 4 chunks of 16 bytes per thread
+template <int NT>
+struct I8Tile {  // NT / 2 rows x 128 bytes, 4 chunks of 16 bytes per thread
     u32x4_t r[4];
     __device__ __forceinline__ void load(rsrc_t rs, int base, int rstep, int col) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) r[i] = bload16(rs, base + i * rstep + col);
     }
     __device__ __forceinline__ void store_part(uint8_t *s, int part) const {
-        const int idx = part * 256 + threadIdx.x;
+        const int idx = part * NT + threadIdx.x;
         *reinterpret_cast<u32x4_t *>(s + i8swz(idx >> 3, idx & 7)) = r[part];
     }
 };
 
-template <int EPI>  // 0: int32 C (or split partials), 1: fp16 C, 2: bf16 C, scaled by sa[m] sb[n]
-__global__ __launch_bounds__(256) void i8_gemm_kernel(const I8Args g) {
-    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][128 * 128];
-    __shared__ __attribute__((aligned(1024))) uint8_t sB[2][128 * 128];
+// BT x BT tiles: 128 (4 waves of 64 x 64, two workgroups per CU) or 256 (8 waves of 128 n x
+// 64 m, one per CU: half the LDS bytes per MFMA).
+template <int EPI, int BT>  // EPI 0: int32 C (or split partials), 1: fp16 C, 2: bf16 C
+__global__ __launch_bounds__(BT * 2) void i8_gemm_kernel(const I8Args g) {
+    constexpr int NT = BT * 2, WN = 2, WM = NT / 64 / WN;
+    constexpr int TN = BT / WN / 32, TM = BT / WM / 32;
+    __shared__ __attribute__((aligned(1024))) uint8_t sA[2][BT * 128];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB[2][BT * 128];
     const uint32_t nsp = static_cast<uint32_t>(g.splits);
     const uint32_t blk = blockIdx.x;
     const uint32_t tile = __builtin_amdgcn_readfirstlane(blk / nsp);
     const int split = __builtin_amdgcn_readfirstlane(static_cast<int>(blk % nsp));
     const uint32_t mtl = static_cast<uint32_t>(g.m_tiles);
-    const int64_t n0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(tile / mtl)) * 128;
-    const int64_t m0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(tile % mtl)) * 128;
+    const int64_t n0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(tile / mtl)) * BT;
+    const int64_t m0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(tile % mtl)) * BT;
     const int64_t steps = g.K / IBR;
     const int64_t s0 = split * g.per_split;
     const int64_t s1 = s0 + g.per_split < steps ? s0 + g.per_split : steps;
 
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int wn = wave & 1, wm = wave >> 1;
+    const int wn = wave % WN, wm = wave / WN;
     const int lane = threadIdx.x & 63, r = lane & 31, kh = lane >> 5;
 
     // windows: rows past M / N read as zero
-    const int64_t ma = g.M - m0 < 128 ? g.M - m0 : 128, nb = g.N - n0 < 128 ? g.N - n0 : 128;
+    const int64_t ma = g.M - m0 < BT ? g.M - m0 : BT, nb = g.N - n0 < BT ? g.N - n0 : BT;
     const rsrc_t ra = make_rsrc(g.a + m0 * g.lda, (ma - 1) * g.lda + g.K);
     const rsrc_t rb = make_rsrc(g.b + n0 * g.ldb, (nb - 1) * g.ldb + g.K);
     const int t = threadIdx.x;
     const int abase = static_cast<int>((t >> 3) * g.lda + (t & 7) * 16);
     const int bbase = static_cast<int>((t >> 3) * g.ldb + (t & 7) * 16);
-    const int astep = static_cast<int>(32 * g.lda), bstep = static_cast<int>(32 * g.ldb);
+    const int astep = static_cast<int>((NT / 8) * g.lda), bstep = static_cast<int>((NT / 8) * g.ldb);
 
-    v16i_t acc[2][2];
+    v16i_t acc[TN][TM];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i_t){};
+        for (int j = 0; j < TM; ++j) acc[i][j] = (v16i_t){};
 
     auto mma = [&](int b, auto &&part) {
 #pragma unroll
         for (int ks = 0; ks < IBR / 32; ++ks) {
             const int c = ks * 2 + kh;
-            v4i_t fn[2], fm[2];
+            v4i_t fn[TN], fm[TM];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                fn[i] = *reinterpret_cast<const v4i_t *>(sB[b] + i8swz(wn * 64 + i * 32 + r, c));
+            for (int i = 0; i < TN; ++i)
+                fn[i] = *reinterpret_cast<const v4i_t *>(sB[b] + i8swz(wn * (BT / WN) + i * 32 + r, c));
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                fm[j] = *reinterpret_cast<const v4i_t *>(sA[b] + i8swz(wm * 64 + j * 32 + r, c));
+            for (int j = 0; j < TM; ++j)
+                fm[j] = *reinterpret_cast<const v4i_t *>(sA[b] + i8swz(wm * (BT / WM) + j * 32 + r, c));
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TN; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TM; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fn[i], fm[j], acc[i][j], 0, 0, 0);
             part(ks);
         }
     };
 
-    I8Tile ta[2], tb[2];
+    I8Tile<NT> ta[2], tb[2];
     if (s0 < s1) {
         ta[0].load(ra, abase, astep, static_cast<int>(s0) * IBR);
         tb[0].load(rb, bbase, bstep, static_cast<int>(s0) * IBR);
@@ -366,17 +371,17 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const I8Args g) {
         if (st < s1) mma(0, [](int) {});
     }
 
-    // epilogue: lane holds C[m][n .. n+3] for m = m0 + wm 64 + j 32 + r, n = n0 + wn 64 + i 32 +
-    // 8 r4 + 4 kh
+    // epilogue: lane holds C[m][n .. n+3] for m = m0 + wm BT/WM + j 32 + r,
+    // n = n0 + wn BT/WN + i 32 + 8 r4 + 4 kh
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int64_t m = m0 + wm * 64 + j * 32 + r;
+    for (int j = 0; j < TM; ++j) {
+        const int64_t m = m0 + wm * (BT / WM) + j * 32 + r;
         if (m >= g.M) continue;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const int64_t n = n0 + wn * 64 + i * 32 + r4 * 8 + kh * 4;
+                const int64_t n = n0 + wn * (BT / WN) + i * 32 + r4 * 8 + kh * 4;
                 if (n >= g.N) continue;
                 const int v[4] = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2],
                                   acc[i][j][4 * r4 + 3]};
@@ -570,21 +575,43 @@ extern "C" int nf4_int8_rows(const void *x, int64_t rows, int64_t cols, int64_t 
 
 namespace {
 
-// Reduction splits: more workgroups than two per CU are not needed; each split keeps >= 8 steps.
-int i8_splits(int64_t tiles, int64_t steps) {
+// Tile size and reduction splits: 256 x 256 tiles (one workgroup per CU) when they fill most of
+// a round, else 128 x 128 (two per CU); splits fill the CUs' places, each keeping >= 8 steps.
+struct I8Plan {
+    int bt;
+    int splits;
+    int64_t m_tiles, tiles;
+};
+
+int i8_splits(int64_t tiles, int64_t steps, int64_t slots) {
     int s = 1;
-    while (s < 16 && tiles * (s + 1) <= 512 && steps / (s + 1) >= 8) ++s;
+    while (s < 16 && tiles * (s + 1) <= slots && steps / (s + 1) >= 8) ++s;
     while (s > 1 && (s - 1) * ((steps + s - 1) / s) >= steps) --s;
     return s;
+}
+
+// Cost: rounds x steps per workgroup x the measured step time (256 x 256: ~2.5 us with one
+// workgroup per CU; 128 x 128: ~1.4 us with two per CU), plus ~10 us for a split's partials
+// and reduction.
+I8Plan i8_plan(int64_t m, int64_t n, int64_t k) {
+    const int64_t steps = k / IBR;
+    const int64_t mt2 = (m + 255) / 256, t2 = mt2 * ((n + 255) / 256);
+    const int64_t mt1 = (m + 127) / 128, t1 = mt1 * ((n + 127) / 128);
+    const int s2 = i8_splits(t2, steps, 256), s1 = i8_splits(t1, steps, 512);
+    auto cost = [&](int64_t tiles, int s, int64_t slots, double t_step) {
+        const int64_t rounds = (tiles * s + slots - 1) / slots;
+        return double(rounds) * double((steps + s - 1) / s) * t_step + (s > 1 ? 10.0 : 0.0);
+    };
+    if (cost(t2, s2, 256, 2.5) < cost(t1, s1, 512, 1.4)) return I8Plan{256, s2, mt2, t2};
+    return I8Plan{128, s1, mt1, t1};
 }
 
 }  // namespace
 
 extern "C" size_t nf4_int8_gemm_workspace(int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0 || k % IBR != 0) return 0;
-    const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-    const int s = i8_splits(tiles, k / IBR);
-    return s > 1 ? static_cast<size_t>(s) * m * n * sizeof(int32_t) : 0;
+    const I8Plan p = i8_plan(m, n, k);
+    return p.splits > 1 ? static_cast<size_t>(p.splits) * m * n * sizeof(int32_t) : 0;
 }
 
 extern "C" int nf4_int8_gemm(const int8_t *a, int64_t m, int64_t lda, const int8_t *b, int64_t n,
@@ -598,8 +625,8 @@ extern "C" int nf4_int8_gemm(const int8_t *a, int64_t m, int64_t lda, const int8
     if (k % IBR != 0 || n % 4 != 0 || lda % 16 != 0 || ldb % 16 != 0 || !aligned(a, 16) ||
         !aligned(b, 16) || ldc % 4 != 0 || !aligned(c, 16))
         return NF4_ERR_UNSUPPORTED;
-    // 32-bit in-window offsets: a 128-row window of either operand below 2 GiB
-    if (128 * lda >= (int64_t(1) << 31) || 128 * ldb >= (int64_t(1) << 31)) return NF4_ERR_UNSUPPORTED;
+    // 32-bit in-window offsets: a 256-row window of either operand below 2 GiB
+    if (256 * lda >= (int64_t(1) << 31) || 256 * ldb >= (int64_t(1) << 31)) return NF4_ERR_UNSUPPORTED;
     I8Args g{};
     g.a = a;
     g.b = b;
@@ -612,10 +639,11 @@ extern "C" int nf4_int8_gemm(const int8_t *a, int64_t m, int64_t lda, const int8
     g.sb = sb;
     g.c = c;
     g.ldc = ldc;
-    g.m_tiles = (m + 127) / 128;
-    const int64_t tiles = g.m_tiles * ((n + 127) / 128);
+    const I8Plan p = i8_plan(m, n, k);
+    g.m_tiles = p.m_tiles;
+    const int64_t tiles = p.tiles;
     const int64_t steps = k / IBR;
-    g.splits = i8_splits(tiles, steps);
+    g.splits = p.splits;
     g.per_split = (steps + g.splits - 1) / g.splits;
     if (g.splits > 1) {
         if (!workspace || workspace_bytes < nf4_int8_gemm_workspace(m, n, k)) return NF4_ERR_WORKSPACE;
@@ -624,9 +652,15 @@ extern "C" int nf4_int8_gemm(const int8_t *a, int64_t m, int64_t lda, const int8
     if (tiles * g.splits > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(tiles * g.splits));
-    if (out_dtype == NF4_I32) hipLaunchKernelGGL(i8_gemm_kernel<0>, grid, dim3(256), 0, st, g);
-    else if (out_dtype == NF4_F16) hipLaunchKernelGGL(i8_gemm_kernel<1>, grid, dim3(256), 0, st, g);
-    else hipLaunchKernelGGL(i8_gemm_kernel<2>, grid, dim3(256), 0, st, g);
+    if (p.bt == 256) {
+        if (out_dtype == NF4_I32) hipLaunchKernelGGL((i8_gemm_kernel<0, 256>), grid, dim3(512), 0, st, g);
+        else if (out_dtype == NF4_F16) hipLaunchKernelGGL((i8_gemm_kernel<1, 256>), grid, dim3(512), 0, st, g);
+        else hipLaunchKernelGGL((i8_gemm_kernel<2, 256>), grid, dim3(512), 0, st, g);
+    } else {
+        if (out_dtype == NF4_I32) hipLaunchKernelGGL((i8_gemm_kernel<0, 128>), grid, dim3(256), 0, st, g);
+        else if (out_dtype == NF4_F16) hipLaunchKernelGGL((i8_gemm_kernel<1, 128>), grid, dim3(256), 0, st, g);
+        else hipLaunchKernelGGL((i8_gemm_kernel<2, 128>), grid, dim3(256), 0, st, g);
+    }
     if (g.splits > 1) {
         if (m > 65535) return NF4_ERR_UNSUPPORTED;
         const dim3 rg(static_cast<unsigned>((n + 255) / 256), static_cast<unsigned>(m));
