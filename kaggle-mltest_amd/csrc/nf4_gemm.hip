@@ -158,6 +158,12 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Tiles run m fastest: the dispatcher deals workgroups to the 8 XCDs in turn (XCD = id mod 8,
+// each with its own L2), so with a multiple of 8 m tiles every XCD keeps the same m tiles and
+// reads its share of the activations once, while the NF4 weight tiles (a quarter of the bytes
+// per element) are read by every XCD.  Grouping a weight tile's m tiles on one XCD instead
+// measured 2x the L2 miss bytes (every XCD then reads all the activations).
+//
 // Workgroup -> (tile, split, number of splits of that tile): 1-D grid of tail_start whole
 // tiles followed by `splits` workgroups per tail tile.  32-bit arithmetic.
 struct BlockTile {
@@ -172,20 +178,6 @@ __device__ __forceinline__ BlockTile block_tile(const GemmArgs &a, uint32_t b) {
     const uint32_t r = b - ts, sp = static_cast<uint32_t>(a.splits);
     return BlockTile{static_cast<int64_t>(__builtin_amdgcn_readfirstlane(ts + r / sp)),
                      static_cast<int>(__builtin_amdgcn_readfirstlane(r % sp)), a.splits};
-}
-
-// Logical workgroup of dispatched workgroup b of n.  The dispatcher deals workgroups to the 8
-// XCDs in turn (XCD b % 8), each XCD with its own L2; within every run of 256 consecutive
-// workgroups (one round of the 256 CUs) XCD x gets a contiguous range of logical tiles, so the
-// m tiles that share a weight tile (m fastest) run on one XCD and read it through one L2.
-// A bijection on every run of 256: rounds keep their tiles.
-__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t n) {
-    constexpr uint32_t kXcds = 8, kRun = 256;
-    const uint32_t c0 = b & ~(kRun - 1);
-    const uint32_t len = n - c0 < kRun ? n - c0 : kRun;
-    const uint32_t j = b - c0, q = len / kXcds, r = len % kXcds;
-    const uint32_t x = j % kXcds, i = j / kXcds;
-    return __builtin_amdgcn_readfirstlane(c0 + (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i);
 }
 
 // The raw absmax inputs of block b, fetched with the packed bytes; rebuilt later by absmax_val.
@@ -890,8 +882,7 @@ template <int DT, int BP, int BM, int WP, int WM, int EPI = 0, int KG = 1>
 __global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<BP, BM, KG>()];
     __shared__ float s_code2[EPI != 0 ? 2 : 1][256];
-    fwd_body<DT, BP, BM, WP, WM, EPI, KG>(a, a.map[0], xcd_tile(blockIdx.x, gridDim.x), lds,
-                                          s_code2);
+    fwd_body<DT, BP, BM, WP, WM, EPI, KG>(a, a.map[0], blockIdx.x, lds, s_code2);
 }
 
 // A two-part launch: workgroups [0, blocks0) run 256x256 tiles over the first part's map, the
@@ -903,11 +894,10 @@ __global__ __launch_bounds__(512) void fwd_head_tail_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
     __shared__ float s_code2[EPI != 0 ? 2 : 1][256];
     const uint32_t b0 = static_cast<uint32_t>(a.blocks0);
-    const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
-    if (t < b0)
-        fwd_body<DT, 256, 256, 2, 4, EPI, 1>(a, a.map[0], t, lds, s_code2);
+    if (blockIdx.x < b0)
+        fwd_body<DT, 256, 256, 2, 4, EPI, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
     else
-        fwd_body<DT, 128, 128, 2, 2, EPI, 2>(a, a.map[1], t - b0, lds, s_code2);
+        fwd_body<DT, 128, 128, 2, 2, EPI, 2>(a, a.map[1], blockIdx.x - b0, lds, s_code2);
 }
 
 // ------------------------------------------------------------------------ decode forward path
@@ -1371,7 +1361,7 @@ template <int DT, int BP, int BM, int WP, int WM, int KG = 1>
 __global__ __launch_bounds__(KG *WP *WM * 64) void dx_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<BP, BM, KG>()];
     __shared__ float s_code2[kMaxSeg][256];
-    dx_body<DT, BP, BM, WP, WM, KG>(a, a.map[0], xcd_tile(blockIdx.x, gridDim.x), lds, s_code2);
+    dx_body<DT, BP, BM, WP, WM, KG>(a, a.map[0], blockIdx.x, lds, s_code2);
 }
 
 // Two-part input-gradient launch (as fwd_head_tail_kernel): output columns of the first part
@@ -1381,11 +1371,10 @@ __global__ __launch_bounds__(512) void dx_head_tail_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
     __shared__ float s_code2[kMaxSeg][256];
     const uint32_t b0 = static_cast<uint32_t>(a.blocks0);
-    const uint32_t t = xcd_tile(blockIdx.x, gridDim.x);
-    if (t < b0)
-        dx_body<DT, 256, 256, 2, 4, 1>(a, a.map[0], t, lds, s_code2);
+    if (blockIdx.x < b0)
+        dx_body<DT, 256, 256, 2, 4, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
     else
-        dx_body<DT, 128, 128, 2, 2, 2>(a, a.map[1], t - b0, lds, s_code2);
+        dx_body<DT, 128, 128, 2, 2, 2>(a, a.map[1], blockIdx.x - b0, lds, s_code2);
 }
 
 // Split reduction over the tail columns [col0, col0 + n_out):
