@@ -494,19 +494,22 @@ struct FwdWeight {
     }
 };
 
-// dX weight tile: 64 rows n x BP columns k of W in its natural layout (rows of BP 16-bit values;
-// 16-byte chunk c of row n at chunk c ^ 4 (n & 3) ^ (n & 1) ^ (c / 16 & 1)).  Thread t
-// dequantizes 32 consecutive k of row t / (BP / 32): one absmax, one register table, four
-// 16-byte LDS writes, as the forward tile.  The MFMA reads it transposed (mma_step_dx below).
-// Rows start on bank 0 (256 or 512 bytes); the bank group of a chunk is its index mod 16.  A
-// 16-byte store serves 8 lanes per pass: one row's chunks 4j + part (j < 8) with BP = 256, two
-// rows' (j < 4) with BP = 128; the two last terms give those 8 chunks 8 different bank groups
-// (without them, 2-way conflicts on every store).  A transposed read covers rows n0 .. n0 + 3
-// (n0 % 4 = 0) and chunks c0 .. c0 + 3 (c0 % 4 = 0): the last terms permute each row's chunks
-// among themselves and the 4 (n & 3) term keeps the rows apart.
+// dX weight tile: 64 rows n x BP columns k of W in its natural layout (rows of BP 16-bit values,
+// 16-byte chunks c swizzled by swz_t).  Thread t dequantizes 32 consecutive k of row
+// t / (BP / 32): one absmax, one register table, four 16-byte LDS writes, as the forward tile.
+// The MFMA reads it transposed (mma_step_dx below).
+//
+// Rows start on bank 0 (256 or 512 bytes), so the bank group of a chunk is its index mod 16, and
+// LDS serves 16 lanes of a 16-byte access per pass.  A store pass covers chunks 4j + part of
+// two rows (j < 8, BP = 256) or of four rows (j < 4, BP = 128); a transposed read pass covers
+// chunks c0 .. c0 + 3 of rows n0 .. n0 + 3 (c0, n0 multiples of 4).  Chunk c of row n goes to
+// c ^ 4 (n & 3) ^ low, where the low two bits separate what the store passes share: c / 16 and
+// row parity for BP = 256, the row mod 4 for BP = 128.  Every pass then hits 16 distinct bank
+// groups (the reads: 4 (n & 3) keeps the rows apart, low only permutes a row's 4 chunks).
 template <int BP>
 __device__ __forceinline__ int swz_t(int n, int c) {
-    return n * (BP * 2) + ((c ^ ((n & 3) << 2) ^ (n & 1) ^ ((c >> 4) & 1)) << 4);
+    const int low = BP == 256 ? (((c >> 4) & 1) ^ ((n & 1) << 1)) : (n & 3);
+    return n * (BP * 2) + ((c ^ ((n & 3) << 2) ^ low) << 4);
 }
 
 template <int BP>
