@@ -136,20 +136,25 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jo
 // Partial sums over a chunk of rows on v_mfma_f32_16x16x32:
 //   part[chunk][p][j] = sum_{m in chunk} U[m][p] * V[m][j]
 // for a 64-column tile of p (4 waves x 16) and one 16-wide tile of j (blockIdx.z).  Both
-// operands are reduced over m, so each 32-row step is staged in LDS transposed ([p][m], [j][m])
-// and the MFMA fragments are contiguous 16-byte LDS reads.
+// operands are reduced over m, so they are staged in LDS transposed ([p][m], [j][m]) and the
+// MFMA fragments are contiguous 16-byte LDS reads.  The chunk runs in blocks of 128 rows: each
+// thread issues the loads of all four 32-row slices of a block before its first LDS store, so a
+// workgroup waits for one memory latency per block; the slices then go through the MFMA in
+// order (the same sums in the same order as one slice at a time).  LDS rows of 136 halves
+// (272 bytes, 17 chunks): the 16 rows of a fragment read start on 16 different bank groups.
 // Grid: x = 64-column p tiles (of the widest job), y = row chunks, z = job x 16-wide j tiles.
 template <int DT>
 __global__ __launch_bounds__(256) void wgrad_partial_kernel(const Jobs jobs, int64_t m, int rank,
                                                             int64_t rows_per_chunk, float *ws) {
-    constexpr int SR = 40;  // LDS row: 32 m + 8 pad (80 bytes)
+    constexpr int MB = 128;     // rows of a block
+    constexpr int SR = MB + 8;  // LDS row (halves)
     __shared__ __attribute__((aligned(16))) uint16_t sU[64 * SR];
     __shared__ __attribute__((aligned(16))) uint16_t sV[16 * SR];
     const int jtiles = (rank + 15) / 16;
     const Job &jb = jobs.j[blockIdx.z / jtiles];
     const uint16_t *u = jb.in, *v = jb.w;
     const int64_t p = jb.cols, ldu = jb.ld;
-    const int vec_u = jb.vec;
+    const bool vec_u = jb.vec != 0;
     float *part = ws + jb.part_off;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 64;
@@ -158,36 +163,44 @@ __global__ __launch_bounds__(256) void wgrad_partial_kernel(const Jobs jobs, int
     const int j0 = (blockIdx.z % jtiles) * 16;
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
+    // U: thread -> 8 columns pc .. pc + 7 of rows ur + 32 s; V: 8 of the 16 j of row vr
+    const int ur = threadIdx.x >> 3, pc = (threadIdx.x & 7) * 8;
+    const int vr = threadIdx.x >> 1, jc = (threadIdx.x & 1) * 8;
+    const int ulim = p - (p0 + pc) < 8 ? static_cast<int>(p - (p0 + pc)) : 8;
+    const int vlim = rank - (j0 + jc) < 8 ? rank - (j0 + jc) : 8;
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t mb = r0; mb < r1; mb += 32) {
-        {   // U[mb .. mb+32][p0 .. p0+64] -> sU[p][m]
-            const int rr = threadIdx.x >> 3, pc = (threadIdx.x & 7) * 8;
-            const int64_t mm = mb + rr, pp = p0 + pc;
-            const int lim = (mm < r1) ? (p - pp < 8 ? static_cast<int>(p - pp) : 8) : 0;
-            const u32x4_t x = lim > 0 ? frag8(u + mm * ldu + pp, 1, lim, vec_u != 0)
-                                      : (u32x4_t){0u, 0u, 0u, 0u};
-            const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+    for (int64_t mb = r0; mb < r1; mb += MB) {
+        u32x4_t xu[MB / 32], xv = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int sl = 0; sl < MB / 32; ++sl) {
+            const int64_t mm = mb + 32 * sl + ur;
+            xu[sl] = (mm < r1 && ulim > 0) ? frag8(u + mm * ldu + p0 + pc, 1, ulim, vec_u)
+                                           : (u32x4_t){0u, 0u, 0u, 0u};
+        }
+        if (mb + vr < r1 && vlim > 0) xv = frag8(v + (mb + vr) * rank + j0 + jc, 1, vlim, false);
+        if (mb > r0) __syncthreads();  // the previous block's fragment reads are done
+#pragma unroll
+        for (int sl = 0; sl < MB / 32; ++sl) {
+            const uint32_t xw[4] = {xu[sl].x, xu[sl].y, xu[sl].z, xu[sl].w};
 #pragma unroll
             for (int q = 0; q < 8; ++q)
-                sU[(pc + q) * SR + rr] = static_cast<uint16_t>(xw[q >> 1] >> ((q & 1) * 16));
+                sU[(pc + q) * SR + 32 * sl + ur] = static_cast<uint16_t>(xw[q >> 1] >> ((q & 1) * 16));
         }
-        if (threadIdx.x < 64) {  // V[mb .. mb+32][j0 .. j0+16] -> sV[j][m]
-            const int rr = threadIdx.x >> 1, jc = (threadIdx.x & 1) * 8;
-            const int64_t mm = mb + rr;
-            const int lim = (mm < r1) ? (rank - (j0 + jc) < 8 ? rank - (j0 + jc) : 8) : 0;
-            const u32x4_t x = lim > 0 ? frag8(v + mm * rank + j0 + jc, 1, lim, false)
-                                      : (u32x4_t){0u, 0u, 0u, 0u};
-            const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+        {
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (int q = 0; q < 8; ++q)
-                sV[(jc + q) * SR + rr] = static_cast<uint16_t>(xw[q >> 1] >> ((q & 1) * 16));
+                sV[(jc + q) * SR + vr] = static_cast<uint16_t>(xw[q >> 1] >> ((q & 1) * 16));
         }
         __syncthreads();
-        const u32x4_t fa = *reinterpret_cast<const u32x4_t *>(sU + (wave * 16 + (lane & 15)) * SR +
-                                                              (lane >> 4) * 8);
-        const u32x4_t fb = *reinterpret_cast<const u32x4_t *>(sV + (lane & 15) * SR + (lane >> 4) * 8);
-        acc = mfma16<DT>(fa, fb, acc);
-        __syncthreads();
+#pragma unroll
+        for (int sl = 0; sl < MB / 32; ++sl) {
+            const int off = 32 * sl + (lane >> 4) * 8;
+            const u32x4_t fa =
+                *reinterpret_cast<const u32x4_t *>(sU + (wave * 16 + (lane & 15)) * SR + off);
+            const u32x4_t fb = *reinterpret_cast<const u32x4_t *>(sV + (lane & 15) * SR + off);
+            acc = mfma16<DT>(fa, fb, acc);
+        }
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
