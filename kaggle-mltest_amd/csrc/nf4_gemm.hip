@@ -1602,14 +1602,15 @@ Plan plan_gemv(int64_t m, const nf4_weight *ws, int nw) {
     return Plan{2, 32, 32 * mt, static_cast<int>(splits), tiles, waves, splits > 1 ? 0 : tiles};
 }
 
-// Decode path: waves per 16-row tile, the most (up to 16) that keep the whole launch resident
+// Decode path: waves per 16-row tile, the most (up to 8) that keep the whole launch resident
 // (kDecodeWavesPerSimd waves per SIMD) and give every wave at least three super-steps (fewer
-// make the cross-wave reduction and the prefetch ramp dominate).
+// make the cross-wave reduction and the prefetch ramp dominate).  16 waves measured slower than
+// 8 where they were allowed (the down projections at M <= 8: 28-layer forward 2-5 % slower).
 Plan plan_decode(const nf4_weight *ws, int nw) {
     int64_t tiles = 0;
     for (int i = 0; i < nw; ++i) tiles += (ws[i].rows + 15) / 16;
     const int64_t ss = ws[0].cols / DK;
-    int waves = 16;
+    int waves = 8;
     while (waves > 1 && (tiles * waves > 4 * kDecodeWavesPerSimd * kCUs || 3 * waves > ss)) waves /= 2;
     return Plan{4, 16, 16, 1, tiles, waves, tiles};
 }
@@ -1663,8 +1664,7 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
     if (p.cfg == 4) {
         const dim3 block(p.waves * 64);
-        if (p.waves == 16) hipLaunchKernelGGL((decode_kernel<DT, 16>), grid, block, 0, st, g);
-        else if (p.waves == 8) hipLaunchKernelGGL((decode_kernel<DT, 8>), grid, block, 0, st, g);
+        if (p.waves == 8) hipLaunchKernelGGL((decode_kernel<DT, 8>), grid, block, 0, st, g);
         else if (p.waves == 4) hipLaunchKernelGGL((decode_kernel<DT, 4>), grid, block, 0, st, g);
         else if (p.waves == 2) hipLaunchKernelGGL((decode_kernel<DT, 2>), grid, block, 0, st, g);
         else hipLaunchKernelGGL((decode_kernel<DT, 1>), grid, block, 0, st, g);

@@ -61,11 +61,13 @@ def test_fused_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape,bs,nested", [((136, 384), 64, True), ((40, 1024), 128, True),
-                                             ((72, 256), 64, False)])
+                                             ((72, 256), 64, False), ((48, 1536), 64, True),
+                                             ((32, 3072), 64, True)])
 def test_decode_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
     """The decode path (M <= 16): 16 one-hot activation rows X = I[c0:c0+16] give the weight
     columns c0 .. c0+15 exactly, for every column block; rows past a 16-row weight tile, plain
-    fp32 absmax and block 128 included."""
+    fp32 absmax and block 128 included.  The reductions of 3 to 24 super-steps give 1, 2, 4 and
+    8 waves per tile (the cross-wave sum in LDS)."""
     from solution import kernels
 
     n, k = shape
