@@ -337,6 +337,8 @@ __global__ __launch_bounds__(64) void qkv_rope_vec_kernel(
 
 // Grid: x = tokens, y = groups of (query or key/value) heads per wave, heads numbered as in
 // qkv_rope_bwd_kernel.
+constexpr int kRopeGroupBatch = 8;
+
 template <int DT>
 __global__ __launch_bounds__(64) void qkv_rope_bwd_vec_kernel(
     const uint16_t *dqe, const uint16_t *dke, const uint16_t *dve, const float *cs, const float *sn,
@@ -370,21 +372,39 @@ __global__ __launch_bounds__(64) void qkv_rope_bwd_vec_kernel(
             const int kv = head - n_heads;
             float k_lo[4] = {0.f, 0.f, 0.f, 0.f}, k_hi[4] = {0.f, 0.f, 0.f, 0.f};
             float v_lo[4] = {0.f, 0.f, 0.f, 0.f}, v_hi[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int r = 0; r < groups; ++r) {
-                const int64_t s = (t * n_heads + kv * groups + r) * head_dim;
-                float e[4];
-                ld4<DT>(dke + s + i, e);
+            // the query heads of this kv head in batches of kRopeGroupBatch: every load of a
+            // batch is issued before its sums (in head order), so the lane waits for one memory
+            // latency per batch instead of one per head
+            for (int r0 = 0; r0 < groups; r0 += kRopeGroupBatch) {
+                u32x2_t e[kRopeGroupBatch][4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) k_lo[j] += e[j];
-                ld4<DT>(dke + s + half + i, e);
+                for (int r = 0; r < kRopeGroupBatch; ++r) {
+                    if (r0 + r >= groups) break;
+                    const int64_t s = (t * n_heads + kv * groups + r0 + r) * head_dim;
+                    e[r][0] = *reinterpret_cast<const u32x2_t *>(dke + s + i);
+                    e[r][1] = *reinterpret_cast<const u32x2_t *>(dke + s + half + i);
+                    e[r][2] = *reinterpret_cast<const u32x2_t *>(dve + s + i);
+                    e[r][3] = *reinterpret_cast<const u32x2_t *>(dve + s + half + i);
+                }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) k_hi[j] += e[j];
-                ld4<DT>(dve + s + i, e);
+                for (int r = 0; r < kRopeGroupBatch; ++r) {
+                    if (r0 + r >= groups) break;
+                    float f[4][4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) v_lo[j] += e[j];
-                ld4<DT>(dve + s + half + i, e);
+                    for (int u = 0; u < 4; ++u) {
+                        f[u][0] = bits_f32<DT>(static_cast<uint16_t>(e[r][u].x & 0xffffu));
+                        f[u][1] = bits_f32<DT>(static_cast<uint16_t>(e[r][u].x >> 16));
+                        f[u][2] = bits_f32<DT>(static_cast<uint16_t>(e[r][u].y & 0xffffu));
+                        f[u][3] = bits_f32<DT>(static_cast<uint16_t>(e[r][u].y >> 16));
+                    }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) v_hi[j] += e[j];
+                    for (int j = 0; j < 4; ++j) {
+                        k_lo[j] += f[0][j];
+                        k_hi[j] += f[1][j];
+                        v_lo[j] += f[2][j];
+                        v_hi[j] += f[3][j];
+                    }
+                }
             }
             const int ko = (n_heads + kv) * head_dim, vo = (n_heads + n_kv + kv) * head_dim;
 #pragma unroll
