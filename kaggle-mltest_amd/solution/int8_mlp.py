@@ -12,16 +12,14 @@ the reference's own int8 tolerance (test_kernels.py:323-357).
 Column scales are computed once per MLP (the reference caches them per module for the run,
 layer.py:598-615); the int8 weights are made from the NF4 bytes at each use, as the fp16 ones
 are.  The reference splits the first GEMM into 512-token chunks to bound a 15 GB GPU's memory;
-one launch covers every token here."""
+one launch covers every token here.  RecomputedMLP's backward takes this path when
+`mlp.INT8_BACKWARD` is set."""
 
 from __future__ import annotations
 
 import torch
 
 from . import kernels
-
-INT8 = True           # int8 input gradients of the MLP (the reference's default)
-INT8_FORWARD = False  # the forward stays fp16 (layer.py:533)
 
 
 def int8_eligible(hidden: int, inter: int, blocksize: int) -> bool:
@@ -64,4 +62,4 @@ def mlp_input_grad_int8(dh2: torch.Tensor, gu: torch.Tensor, gate, up, down,
                              out_dtype=dtype)
 
 
-__all__ = ["INT8", "INT8_FORWARD", "int8_eligible", "ColumnScales", "mlp_input_grad_int8"]
+__all__ = ["int8_eligible", "ColumnScales", "mlp_input_grad_int8"]

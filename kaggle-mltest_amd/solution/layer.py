@@ -122,7 +122,11 @@ class NF4Projection(torch.autograd.Function):
         spec = ctx.spec
         dy = _aligned_rows(dy.to(x.dtype))
         offs = spec.offsets()
-        grads, structs, da_jobs, wg_jobs, pairs = [], [], [], [], []
+        # `live` holds every tensor the launches below reach only through raw pointers in
+        # their argument structs, until the last launch is queued: a tensor freed earlier
+        # goes back to torch's allocator, which may hand its memory to the next allocation
+        # while a queued kernel still reads it
+        grads, structs, da_jobs, wg_jobs, pairs, live = [], [], [], [], [], []
         for i, ad in enumerate(spec.loras):
             t, a16, b16 = saved[3 * i: 3 * i + 3]
             r = a16.shape[0]
@@ -131,6 +135,7 @@ class NF4Projection(torch.autograd.Function):
             if dy_s.data_ptr() % 16:
                 dy_s = dy_s.contiguous()
             da = torch.empty((x.shape[0], r), dtype=x.dtype, device=x.device)
+            live.append(da)
             grad_b = torch.empty((rows, r), dtype=torch.float32, device=x.device)
             grad_a = torch.empty((r, x.shape[1]), dtype=torch.float32, device=x.device)
             da_jobs.append((r, kernels.lora_job(dy_s, b16, da, ad.scale)))

@@ -10,14 +10,21 @@ pair, summed in fp32 (the reference adds two fp16 products).  Below FUSED_MIN_TO
 (decode) the unfused sequence runs: the stacked small-M GEMM, then the SwiGLU kernels.
 The reference's recompute budget (mlp.py:92-120) is a 15 GB-GPU memory policy and is not
 mirrored: this MLP always recomputes.
+
+`INT8_BACKWARD` (off by default, as RecomputedMLP's backward is fp16 in the reference) routes the
+input gradient through the int8 GEMMs of `int8_mlp` instead, the way the reference's fused
+decoder layer runs its MLP backward on the T4 (layer.py:530-534, 992-1013).
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import kernels
+from . import _lib, kernels
 from .quant_state import nf4_state_ok
+
+# int8 input gradients (int8_mlp.mlp_input_grad_int8) in RecomputedMLP.backward
+INT8_BACKWARD = False
 
 
 # Token count from which the gate|up GEMM carries the SwiGLU epilogue (its tiles are the large
@@ -53,6 +60,14 @@ class RecomputedMLP(torch.autograd.Function):
         grad = grad.reshape(-1, grad.shape[-1]).to(x2.dtype)
         if grad.stride(0) % 8 or grad.data_ptr() % 16:
             grad = grad.contiguous()
+        if INT8_BACKWARD and _int8_ok(gate_qs, down_qs):
+            from .int8_mlp import mlp_input_grad_int8
+
+            gate, up, down = (gate_w, gate_qs), (up_w, up_qs), (down_w, down_qs)
+            gu = kernels.linear_fwd(x2, [gate, up])
+            dx = mlp_input_grad_int8(grad, gu, gate, up, down,
+                                     scales=_SCALES.get(gate, up, down, x2.dtype))
+            return dx.view(ctx.shape), None, None, None, None, None, None
         d_hidden = kernels.linear_dx(grad, [(down_w, down_qs)])
         if x2.shape[0] >= FUSED_MIN_TOKENS:
             gu = kernels.linear_swiglu_bwd(x2, (gate_w, gate_qs), (up_w, up_qs), d_hidden)
@@ -64,6 +79,31 @@ class RecomputedMLP(torch.autograd.Function):
         del d_hidden
         dx = kernels.linear_dx(gu, [(gate_w, gate_qs), (up_w, up_qs)])
         return dx.view(ctx.shape), None, None, None, None, None, None
+
+
+def _int8_ok(gate_qs, down_qs) -> bool:
+    from .int8_mlp import int8_eligible
+
+    return int8_eligible(int(gate_qs.shape[1]), int(gate_qs.shape[0]), int(gate_qs.blocksize)) \
+        and int(down_qs.blocksize) <= 128 and 128 % int(down_qs.blocksize) == 0
+
+
+class _Scales:
+    """The int8 column scales of each MLP, made once per weight triple (the weights are
+    frozen; the reference caches them per module for the run, layer.py:598-615)."""
+
+    def __init__(self):
+        self._cols = None
+
+    def get(self, gate, up, down, dtype):
+        if self._cols is None:
+            from .int8_mlp import ColumnScales
+
+            self._cols = ColumnScales()
+        return self._cols.get(gate, up, down, dtype)
+
+
+_SCALES = _Scales()
 
 
 def _usable(layer, in_features):
@@ -79,9 +119,12 @@ def _usable(layer, in_features):
 
 def patch_qwen2_mlp_recompute():
     """Qwen2MLP.forward through RecomputedMLP under fp16 autocast (mlp.py:123-157).  Needs
-    bitsandbytes (the layers it serves are Linear4bit); raises ImportError without it."""
+    bitsandbytes (the layers it serves are Linear4bit) and a loadable libnf4_mi355x.so; raises
+    without either (apply() logs that and leaves Qwen2MLP.forward as it was)."""
     import bitsandbytes  # noqa: F401 - the layers this patch serves are bitsandbytes layers
     from transformers.models.qwen2 import modeling_qwen2
+
+    _lib.load()
 
     cls = modeling_qwen2.Qwen2MLP
     if getattr(cls.forward, "_nf4_recompute", False):

@@ -11,19 +11,38 @@ to HBM.
 Differences from the reference, by design:
 * the double-quantized absmax is rebuilt inside the kernels from the uint8 codes (no cached
   fp32 absmax, nf4.py:41-55), bit for bit the same value;
-* the GEMM runs in fp16 or bf16 only; an fp32 GEMM (the reference's path when neither autocast
-  nor a half compute dtype is set) is left to bitsandbytes' original forward.
+* fp16 and bf16 GEMMs are one fused launch; an fp32 GEMM (the reference's path when neither
+  autocast nor a half compute dtype is set) dequantizes to fp32 with the HIP kernel and
+  multiplies with torch's fp32 GEMM, as the reference's NF4Linear does in fp32;
+* a library that cannot be loaded, or an error status from it, sends the call to
+  bitsandbytes' original function instead of raising (the reference's patches never raise:
+  __init__.py:49-53, nf4.py:172-181).
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import kernels
-from ._lib import NF4Unsupported
+from . import _lib, kernels
+from ._lib import NF4LibraryError
 from .quant_state import nf4_state_ok
 
 DEQUANT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+LINEAR_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _gemm_rows(t):
+    """t [M, C] as the fused GEMMs read their activations: unit column stride, a row stride
+    that is a multiple of 8 elements and a 16-byte aligned start.  Anything else is copied
+    into a fresh [M, C rounded up to 8] buffer (zero padding) and returned as its [M, C] view,
+    so an output width that is not a multiple of 8 (e.g. 100) still has an input gradient."""
+    if t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    m, c = t.shape
+    c8 = -(-c // 8) * 8
+    buf = t.new_zeros((m, c8)) if c8 != c else t.new_empty((m, c8))
+    buf[:, :c] = t
+    return buf[:, :c]
 
 
 def dequantize_nf4(packed, quant_state, dtype=torch.float16):
@@ -41,28 +60,39 @@ class NF4Linear(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, packed, quant_state, bias):
-        if x.dtype not in kernels.GEMM_DTYPES:
-            raise TypeError(f"NF4Linear computes in fp16 or bf16, got {x.dtype}")
+        if x.dtype not in LINEAR_DTYPES:
+            raise TypeError(f"NF4Linear computes in fp16, bf16 or fp32, got {x.dtype}")
         shape = x.shape
-        x2 = x.reshape(-1, shape[-1])
-        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-            x2 = x2.contiguous()
         packed = packed.reshape(-1)
-        b = None if bias is None else bias.to(x.dtype).contiguous()
-        out = kernels.linear_fwd(x2, [(packed, quant_state)], b)
+        if x.dtype == torch.float32:
+            # fp32: the weight dequantized to fp32 by the HIP kernel, torch's fp32 GEMM
+            # (nf4.py:86-87 with x in fp32)
+            w = dequantize_nf4(packed, quant_state, torch.float32)
+            out = torch.nn.functional.linear(x, w, None if bias is None else bias.float())
+        else:
+            x2 = _gemm_rows(x.reshape(-1, shape[-1]))
+            b = None if bias is None else bias.to(x.dtype).contiguous()
+            out = kernels.linear_fwd(x2, [(packed, quant_state)], b)
+            out = out.view(*shape[:-1], out.shape[-1])
         ctx.quant_state = quant_state
         ctx.has_bias_grad = bias is not None and ctx.needs_input_grad[3]
         ctx.bias_dtype = None if bias is None else bias.dtype
         ctx.save_for_backward(packed)
-        return out.view(*shape[:-1], out.shape[-1])
+        return out
 
     @staticmethod
     def backward(ctx, grad):
         (packed,) = ctx.saved_tensors
         grad_x = grad_bias = None
         g2 = grad.reshape(-1, grad.shape[-1])
-        if g2.stride(-1) != 1 or g2.stride(0) % 8 or g2.data_ptr() % 16:
-            g2 = g2.contiguous()
+        if grad.dtype == torch.float32:
+            if ctx.needs_input_grad[0]:
+                w = dequantize_nf4(packed, ctx.quant_state, torch.float32)
+                grad_x = torch.matmul(grad, w)
+            if ctx.has_bias_grad:
+                grad_bias = g2.sum(0).to(ctx.bias_dtype)
+            return grad_x, None, None, grad_bias
+        g2 = _gemm_rows(g2)
         if ctx.needs_input_grad[0]:
             dx = kernels.linear_dx(g2, [(packed, ctx.quant_state)])
             grad_x = dx.view(*grad.shape[:-1], dx.shape[-1])
@@ -112,9 +142,18 @@ def _fused_ok(quant_state) -> bool:
 
 
 def _supported(x, packed, quant_state):
-    return (x.is_cuda and x.numel() > 0 and x.dtype in (torch.float16, torch.float32,
-                                                        torch.bfloat16)
-            and _nf4_state_ok(packed, quant_state, x.shape[-1]) and _fused_ok(quant_state))
+    """nf4.py:134-137 (fp16 / fp32 inputs), plus bf16."""
+    return (x.is_cuda and x.numel() > 0 and x.dtype in LINEAR_DTYPES
+            and _nf4_state_ok(packed, quant_state, x.shape[-1]))
+
+
+def _routable(gemm_dtype, quant_state) -> bool:
+    """Whether this path runs a GEMM in `gemm_dtype` on this weight: fp16 / bf16 through the
+    fused kernels (the layouts `_fused_ok` covers), fp32 through the dequant kernel and torch's
+    fp32 GEMM (any even blocksize)."""
+    if gemm_dtype == torch.float32:
+        return True
+    return gemm_dtype in kernels.GEMM_DTYPES and _fused_ok(quant_state)
 
 
 def _gemm_dtype(module, x):
@@ -126,10 +165,12 @@ def _gemm_dtype(module, x):
 
 
 def patch_linear4bit():
-    """Linear4bit.forward through NF4Linear (nf4.py:148-195).  Needs bitsandbytes; raises
-    ImportError without it (apply() logs that and goes on)."""
+    """Linear4bit.forward through NF4Linear (nf4.py:148-195).  Needs bitsandbytes and a
+    loadable libnf4_mi355x.so; raises without either (apply() logs that and goes on, leaving
+    bitsandbytes' forward in place)."""
     from bitsandbytes.nn import modules as bnb_modules
 
+    _lib.load()
     cls = bnb_modules.Linear4bit
     if getattr(cls.forward, "_nf4_patched", False):
         return
@@ -148,11 +189,11 @@ def patch_linear4bit():
             self.compute_type_is_set = True
         gemm_dtype = _gemm_dtype(self, x)
         base_dtype = self.compute_dtype or x.dtype
-        if gemm_dtype not in kernels.GEMM_DTYPES or \
+        if not _routable(gemm_dtype, quant_state) or \
                 _base_uses_fused_kernel(x, quant_state, base_dtype):
             return original(self, x)
         half = getattr(x, "_soup_half", None)
-        x = half if half is not None and half.dtype == gemm_dtype and half.shape == x.shape \
+        xg = half if half is not None and half.dtype == gemm_dtype and half.shape == x.shape \
             else x.to(gemm_dtype)
         bias = self.bias
         if bias is not None:
@@ -160,8 +201,8 @@ def patch_linear4bit():
                 bias.data = bias.data.to(base_dtype)
             bias = bias.to(gemm_dtype)
         try:
-            return NF4Linear.apply(x, self.weight.view(-1), quant_state, bias)
-        except NF4Unsupported:
+            return NF4Linear.apply(xg, self.weight.view(-1), quant_state, bias)
+        except NF4LibraryError:  # unsupported layout or a HIP error: bitsandbytes' path
             return original(self, x)
 
     forward._nf4_patched = True
@@ -169,21 +210,23 @@ def patch_linear4bit():
 
 
 def patch_bnb_matmul_4bit():
-    """bitsandbytes.matmul_4bit through NF4Linear (nf4.py:198-216)."""
+    """bitsandbytes.matmul_4bit through NF4Linear (nf4.py:198-216).  Needs bitsandbytes and a
+    loadable libnf4_mi355x.so."""
     import bitsandbytes
     from bitsandbytes.autograd import _functions as bnb_autograd
 
+    _lib.load()
     if getattr(bitsandbytes.matmul_4bit, "_nf4_patched", False):
         return
     original = bitsandbytes.matmul_4bit
 
     def matmul_4bit(A, B, quant_state, out=None, bias=None):
         if out is not None or not _supported(A, B, quant_state) or \
-                A.dtype not in kernels.GEMM_DTYPES or _base_uses_fused_kernel(A, quant_state):
+                not _routable(A.dtype, quant_state) or _base_uses_fused_kernel(A, quant_state):
             return original(A, B, quant_state, out=out, bias=bias)
         try:
             return NF4Linear.apply(A, B.view(-1), quant_state, bias)
-        except NF4Unsupported:
+        except NF4LibraryError:  # unsupported layout or a HIP error: bitsandbytes' path
             return original(A, B, quant_state, out=out, bias=bias)
 
     matmul_4bit._nf4_patched = True

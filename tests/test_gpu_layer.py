@@ -100,3 +100,40 @@ def test_recomputed_mlp_matches_fp32(cuda, tokens):
     ref.backward(grad.float().cpu())
     assert_rel(out, ref.detach(), what="mlp out")
     assert_rel(x.grad, xr.grad, what="mlp dx")
+
+
+def test_projection_backward_with_dirty_allocator_cache(cuda):
+    """The backward's LoRA side buffers (da) are reached by the kernels only through raw
+    pointers: they must stay allocated until the last launch is queued.  torch's cache is first
+    filled with NaN so that a buffer freed too early and handed to another allocation shows as
+    NaN in dX (it once did, on the second of two runs)."""
+    from solution.layer import LoraAdapter, ProjectionSpec, project
+
+    banner("NF4Projection backward, NaN-filled allocator cache")
+    m, k, r, s = 512, 1536, 16, 2.0
+    segs = [random_weight(n, k, seed=100 + i, dev=cuda) for i, n in enumerate((1536, 256, 256))]
+    w = torch.cat([oracle_w16(pp, q) for pp, q in segs]).float()
+    g = torch.Generator().manual_seed(7)
+    x0 = torch.randn(m, k, generator=g).half()
+    dy = (torch.randn(m, 2048, generator=g) * 1e-3).half()
+    params0 = [(torch.rand(r, k, generator=g) - 0.5) * 0.05, torch.randn(1536, r, generator=g) * 0.01,
+               (torch.rand(r, k, generator=g) - 0.5) * 0.05, torch.randn(256, r, generator=g) * 0.01]
+    spec = ProjectionSpec(weights=segs, loras=[LoraAdapter(0, s), LoraAdapter(2, s)])
+    xr = x0.float().requires_grad_()
+    leaves = [p.clone().requires_grad_() for p in params0]
+    aq, bq, av, bv = leaves
+    yr = xr @ w.t()
+    yr = torch.cat([yr[:, :1536] + s * (xr @ aq.t()) @ bq.t(), yr[:, 1536:1792],
+                    yr[:, 1792:] + s * (xr @ av.t()) @ bv.t()], -1)
+    yr.backward(dy.float())
+    for _ in range(3):
+        torch.full((1 << 28,), float("nan"), dtype=torch.float16, device=cuda)  # freed at once
+        x = x0.to(cuda).requires_grad_()
+        params = [p.to(cuda).requires_grad_() for p in params0]
+        y = project(x, spec, None, params)
+        torch.full((1 << 28,), float("nan"), dtype=torch.float16, device=cuda)
+        y.backward(dy.to(cuda))
+        torch.cuda.synchronize()
+        assert_rel(x.grad, xr.grad, what="dx")
+        for name, p, ref in zip(("dA_q", "dB_q", "dA_v", "dB_v"), params, leaves):
+            assert_rel(p.grad, ref.grad, what=name)

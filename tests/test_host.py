@@ -126,3 +126,31 @@ def test_cu_seqlens_validation():
     for bad in ([1, 5], [0, 5, 3], [[0, 1]]):
         with pytest.raises(ValueError):
             tokens_from_cu_seqlens(bad)
+
+
+@pytest.mark.parametrize("junk", [False, True])
+def test_apply_with_unloadable_library_keeps_bitsandbytes(monkeypatch, capsys, tmp_path, junk):
+    """A library that is missing or does not load: every patch is skipped and logged, and
+    bitsandbytes' functions (here the stand-in's) stay in place (__init__.py:49-53)."""
+    from transformers.models.qwen2 import modeling_qwen2
+
+    import solution
+    from solution import _lib
+    from tests import bnb_standin
+
+    bnb, _ = bnb_standin.install(monkeypatch)
+    path = tmp_path / "libnf4_mi355x.so"
+    if junk:
+        path.write_bytes(b"not an ELF file")
+    monkeypatch.setattr(_lib, "LIB_PATH", path)
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(modeling_qwen2.Qwen2MLP, "forward", modeling_qwen2.Qwen2MLP.forward)
+    before = (bnb.nn.modules.Linear4bit.forward, bnb.matmul_4bit,
+              bnb.autograd._functions.matmul_4bit, modeling_qwen2.Qwen2MLP.forward)
+    done = solution.apply()
+    assert not any(done.values())
+    after = (bnb.nn.modules.Linear4bit.forward, bnb.matmul_4bit,
+             bnb.autograd._functions.matmul_4bit, modeling_qwen2.Qwen2MLP.forward)
+    assert after == before
+    err = capsys.readouterr().err
+    assert err.count("not applied: NF4LibraryError") == 3, err

@@ -260,6 +260,24 @@ def test_qkv_rope_identity_norms_and_expansion():
     assert torch.equal(vc.reshape(3, -1), qkv[:, (nh + nkv) * hd:])
 
 
+def test_qkv_rope_sign_known_answer():
+    """The rotation's sign convention (layer.py:196-197, the rotate-half form of Qwen2's
+    apply_rotary_pos_emb): at cos = 0, sin = 1 every pair (lo, hi) becomes (-hi, lo); at
+    cos = 0, sin = -1 it becomes (hi, -lo).  An exchanged or flipped sign fails one of the two."""
+    import torch
+
+    qkv, cos, sin = _rope_inputs(seed=7)
+    nh, nkv, hd = 6, 2, 8
+    half = hd // 2
+    for s in (1.0, -1.0):
+        q, k, _, kc, _ = o.qkv_rope(qkv, torch.zeros_like(cos), torch.full_like(sin, s), nh, nkv, hd)
+        qin = qkv[:, :nh * hd].reshape(3, nh, hd)
+        kin = qkv[:, nh * hd:(nh + nkv) * hd].reshape(3, nkv, hd)
+        for got, src in ((q, qin), (kc, kin)):
+            assert torch.equal(got[..., :half], -s * src[..., half:])
+            assert torch.equal(got[..., half:], s * src[..., :half])
+
+
 def test_qkv_rope_bwd_matches_autograd():
     import torch
 
