@@ -98,6 +98,24 @@ int nf4_dequant_multi(const nf4_weight *ws, int nw, void *out, int out_dtype, vo
 int nf4_dequant_batch(const nf4_weight *ws, int nw, void *const *outs, int out_dtype,
                       void *stream);
 
+/* Any number of weights dequantized by ONE launch through a descriptor table (e.g. all 196
+ * projections of a 28-layer model).  The weights are frozen, so the table is built once:
+ * nf4_dequant_table_pack validates every weight (fast layout: power-of-two blocksize >= 8,
+ * 4-byte aligned packed bytes, 16-byte aligned outputs, < 2^32 elements each; else
+ * NF4_ERR_UNSUPPORTED) and writes the table into HOST memory of nf4_dequant_table_bytes()
+ * bytes, with the launch's workgroup count in *blocks.  The caller copies the table to device
+ * memory (64-byte aligned) once; nf4_dequant_table then launches on that copy with the same nw
+ * and blocks, any number of times, writing weight i into outs[i] as nf4_dequant_batch would.
+ * The kernel checks the table's tag, dtype, weight and workgroup counts and writes nothing
+ * when they do not match the launch.
+ * Replaces: a sequence of dequantize_nf4 / _dequant calls, one launch per call
+ *           (/root/reference/solution/nf4.py:69-77; layer.py:463-493). */
+size_t nf4_dequant_table_bytes(const nf4_weight *ws, int nw);
+int nf4_dequant_table_pack(const nf4_weight *ws, int nw, void *const *outs, int out_dtype,
+                           void *host_table, size_t table_bytes, int64_t *blocks);
+int nf4_dequant_table(const void *dev_table, int nw, int64_t blocks, int out_dtype,
+                      void *stream);
+
 /* ------------------------------------------------------------------ fused dequant-GEMMs */
 
 /* Y[M, sum(rows)] = X[M, K] @ W_stack^T (+ bias) (+ sum over loras scale * T @ B^T on the

@@ -9,6 +9,8 @@
 // flight.  The NF4 table and the 256-entry absmax code map sit in LDS.  The absmax is rebuilt
 // per unit from its uint8 code, never materialised in HBM.
 
+#include <cstring>
+
 #include "nf4_common.h"
 
 namespace {
@@ -24,11 +26,16 @@ struct DequantArgs {
 };
 
 // 8 consecutive outputs, streamed (non-temporal: the weight is written once, read later by
-// another kernel).
+// another kernel), through global-address-space pointers: a generic (flat) store may alias LDS,
+// so the compiler orders it against the next unit's LDS table reads by waiting for every store
+// to complete; a global store only waits for the loads the next unit needs.
+typedef __attribute__((address_space(1))) u32x4_t g_u32x4_t;
+typedef __attribute__((address_space(1))) float4_t g_float4_t;
+
 template <int DT>
 __device__ __forceinline__ void store8(void *out, int64_t e, const float (&v)[8]) {
     if constexpr (DT == NF4_F32) {
-        float4_t *o = reinterpret_cast<float4_t *>(static_cast<float *>(out) + e);
+        g_float4_t *o = (g_float4_t *)(static_cast<float *>(out) + e);
         __builtin_nontemporal_store((float4_t){v[0], v[1], v[2], v[3]}, o);
         __builtin_nontemporal_store((float4_t){v[4], v[5], v[6], v[7]}, o + 1);
     } else {
@@ -37,7 +44,7 @@ __device__ __forceinline__ void store8(void *out, int64_t e, const float (&v)[8]
         r.y = pack2<DT>(v[2], v[3]);
         r.z = pack2<DT>(v[4], v[5]);
         r.w = pack2<DT>(v[6], v[7]);
-        __builtin_nontemporal_store(r, reinterpret_cast<u32x4_t *>(static_cast<uint16_t *>(out) + e));
+        __builtin_nontemporal_store(r, (g_u32x4_t *)(static_cast<uint16_t *>(out) + e));
     }
 }
 
@@ -62,22 +69,32 @@ __device__ __forceinline__ int find_segment(const DequantArgs &a, int64_t blk) {
 // 4-byte aligned packed pointer, a 16-byte aligned output start and fewer than 2^32 elements.
 // All loads of a thread (packed units, uint8 absmax codes, absmax2 scales) are issued first,
 // through buffer resources (past the end reads zero, so they need no branches), then the
-// tables; one wait covers them all.  Elements past the last full unit are done one by one.
+// tables; one wait covers them all.  The elements past the last full unit are done one by one
+// after the store loop (loads inside that loop would make every store wait for completion).
+// `lb`: the workgroup's index inside its weight; `wref` is read once into registers.
 template <int DT>
-__global__ __launch_bounds__(kThreads) void dequant_units_kernel(const DequantArgs a) {
-    __shared__ float s_code[16];
-    __shared__ float s_code2[256];
-    const int seg = find_segment(a, blockIdx.x);
-    const DevWeight &w = a.w[seg];
+__device__ __forceinline__ void dequant_units_body(const DevWeight &wref, void *out, int64_t lb,
+                                                   float *s_code, float *s_code2) {
+    const DevWeight w = wref;
     const int64_t n = w.rows * w.cols;
     const int64_t units = n >> 3;
     const int64_t nb = (n + w.blocksize - 1) >> w.bs_shift;
-    const int64_t lb = static_cast<int64_t>(blockIdx.x) - a.block_start[seg];
+    // Branch-free over the absmax format: nested weights read a uint8 code and an absmax2
+    // scale per block group; a plain weight reads code 0 from an empty resource and its fp32
+    // absmax as the "scale", with a code2 table of {1, 0, ..} and offset 0, so that
+    // 1 * absmax + 0 returns the stored absmax exactly.
     const rsrc_t pk = make_rsrc(w.packed, units * 4);
-    const rsrc_t qr = make_rsrc(w.absmax, w.nested ? nb : nb * 4);
+    const rsrc_t qr = make_rsrc(w.absmax, w.nested ? nb : 0);
     const rsrc_t sr = w.nested ? make_rsrc(w.absmax2, ((nb + w.blocksize2 - 1) >> w.bs2_shift) * 4)
-                               : qr;
-
+                               : make_rsrc(w.absmax, nb * 4);
+    const int sshift = w.nested ? w.bs2_shift : 0;
+    const float offset = w.nested ? w.offset : 0.0f;
+    // table entries first: their wait before the LDS fill then does not wait for the data
+    const rsrc_t cr = make_rsrc(w.code, 16 * 4);
+    const rsrc_t c2r = make_rsrc(w.code2, w.nested ? 256 * 4 : 0);
+    const float ct = __builtin_bit_cast(float, bload4(cr, static_cast<int>(threadIdx.x % 16) * 4));
+    float c2t = __builtin_bit_cast(float, bload4(c2r, static_cast<int>(threadIdx.x) * 4));
+    if (!w.nested && threadIdx.x == 0) c2t = 1.0f;
     uint32_t p[kUnroll], q[kUnroll];
     float sc[kUnroll];
     const uint32_t u0 = static_cast<uint32_t>(lb * (kUnroll * kThreads)) + threadIdx.x;
@@ -86,41 +103,100 @@ __global__ __launch_bounds__(kThreads) void dequant_units_kernel(const DequantAr
         const uint32_t u = u0 + g * kThreads;
         p[g] = bload4(pk, static_cast<int>(u * 4));
         const uint32_t b = (u << 3) >> w.bs_shift;
-        if (w.nested) {
-            q[g] = bload1(qr, static_cast<int>(b));
-            sc[g] = __builtin_bit_cast(float, bload4(sr, static_cast<int>((b >> w.bs2_shift) * 4)));
-        } else {
-            q[g] = 0;
-            sc[g] = __builtin_bit_cast(float, bload4(qr, static_cast<int>(b * 4)));
-        }
+        q[g] = bload1(qr, static_cast<int>(b));
+        sc[g] = __builtin_bit_cast(float, bload4(sr, static_cast<int>((b >> sshift) * 4)));
     }
-    if (threadIdx.x < 16) s_code[threadIdx.x] = w.code[threadIdx.x];
-    if (w.nested) s_code2[threadIdx.x] = w.code2[threadIdx.x];
+    if (threadIdx.x < 16) s_code[threadIdx.x] = ct;
+    s_code2[threadIdx.x] = c2t;
     __syncthreads();
 
-    void *out = a.out[seg];
-    const int64_t off = 0;
 #pragma unroll
     for (int g = 0; g < kUnroll; ++g) {
         const int64_t u = u0 + g * kThreads;
         if (u < units) {
-            const float s = w.nested ? __fadd_rn(__fmul_rn(s_code2[q[g]], sc[g]), w.offset) : sc[g];
+            const float s = __fadd_rn(__fmul_rn(s_code2[q[g]], sc[g]), offset);
             float v[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 v[2 * j] = __fmul_rn(s_code[(p[g] >> (8 * j + 4)) & 0xF], s);
                 v[2 * j + 1] = __fmul_rn(s_code[(p[g] >> (8 * j)) & 0xF], s);
             }
-            store8<DT>(out, off + (u << 3), v);
-        } else if (u == units && (n & 7)) {
-            for (int64_t e = units << 3; e < n; ++e) {
-                const uint8_t byte = w.packed[e >> 1];
-                const int nib = (e & 1) ? (byte & 0xF) : (byte >> 4);
-                const float s = absmax_of(w, s_code2, block_index(w, e));
-                store1<DT>(out, off + e, __fmul_rn(s_code[nib], s));
-            }
+            store8<DT>(out, u << 3, v);
         }
     }
+    // the partial unit at the end of the weight: the thread that owns unit `units`
+    const int64_t tail = units - static_cast<int64_t>(u0);
+    if ((n & 7) && tail >= 0 && tail < int64_t(kUnroll) * kThreads && tail % kThreads == 0) {
+        for (int64_t e = units << 3; e < n; ++e) {
+            const uint8_t byte = w.packed[e >> 1];
+            const int nib = (e & 1) ? (byte & 0xF) : (byte >> 4);
+            const float s = absmax_of(w, s_code2, block_index(w, e));
+            store1<DT>(out, e, __fmul_rn(s_code[nib], s));
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void dequant_units_kernel(const DequantArgs a) {
+    __shared__ float s_code[16];
+    __shared__ float s_code2[256];
+    const int seg = find_segment(a, blockIdx.x);
+    dequant_units_body<DT>(a.w[seg], a.out[seg],
+                           static_cast<int64_t>(blockIdx.x) - a.block_start[seg], s_code, s_code2);
+}
+
+// ------------------------------------------------------------ descriptor-table launches
+//
+// Any number of weights in one launch: the host packs a table once (the weights are frozen),
+// the caller copies it to device memory, and every launch reads it there.  Layout: a header,
+// one entry per weight, then one uint32 per workgroup naming its weight.  The offsets follow
+// from the weight count, so the launch passes the index and the entries directly: a workgroup
+// loads the header and its index word together (one scalar round trip), checks the header (tag,
+// dtype, weight and workgroup counts; a table that does not match the launch writes nothing),
+// then loads its entry (a second round trip) and the weight's data.  On the 196 weights of a
+// 28-layer Qwen2.5-1.5B stack (3.3 GB per pass) one launch runs at 5.7 TB/s, against 5.1 TB/s
+// for one nf4_dequant_batch launch per layer; most of the gain came from the store loop of
+// dequant_units_body (global stores, no loads inside the loop), which both paths share.
+
+constexpr uint32_t kTableTag = 0x4e463454u;  // "NF4T"
+
+struct TableHeader {
+    uint32_t tag;
+    int32_t nw;
+    int32_t out_dtype;
+    int32_t pad;
+    int64_t blocks;      // workgroups of the launch
+    int64_t entries;     // byte offset of the entries
+    int64_t index;       // byte offset of the per-workgroup weight index
+    int64_t pad2[3];
+};
+
+struct __attribute__((aligned(16))) TableEntry {
+    DevWeight w;
+    void *out;
+    int64_t block_start;  // first workgroup of this weight
+};
+
+int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+int64_t table_entries_offset() { return align_up(sizeof(TableHeader), 64); }
+int64_t table_index_offset(int nw) {
+    return align_up(table_entries_offset() + static_cast<int64_t>(nw) * sizeof(TableEntry), 64);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void dequant_table_kernel(const TableHeader *h,
+                                                                 const TableEntry *entries,
+                                                                 const uint32_t *index, int nw,
+                                                                 int64_t blocks) {
+    __shared__ float s_code[16];
+    __shared__ float s_code2[256];
+    const uint32_t idx = index[blockIdx.x];
+    if (h->tag != kTableTag || h->out_dtype != DT || h->blocks != blocks || h->nw != nw ||
+        idx >= static_cast<uint32_t>(nw))
+        return;
+    const TableEntry &e = entries[idx];
+    dequant_units_body<DT>(e.w, e.out, static_cast<int64_t>(blockIdx.x) - e.block_start, s_code,
+                           s_code2);
 }
 
 // General path (any even blocksize, any alignment): one element per thread, grid-stride.
@@ -165,6 +241,26 @@ int launch(DequantArgs &a, int path, int dt, hipStream_t stream) {
 }
 
 
+// The fast path's conditions on one weight and its output.
+bool units_layout_ok(const nf4_weight &w, const void *out) {
+    const int64_t n = w.rows * w.cols;
+    return w.blocksize >= 8 && log2_exact(w.blocksize) >= 0 &&
+           (!w.nested || log2_exact(w.blocksize2) >= 0) && aligned(w.packed, 4) &&
+           aligned(out, 16) && n < (int64_t(1) << 32);
+}
+
+int64_t units_blocks(const nf4_weight &w) {
+    const int64_t n = w.rows * w.cols;
+    const int64_t units = (n >> 3) + ((n & 7) ? 1 : 0);
+    return (units + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+}
+
+int64_t table_blocks(const nf4_weight *ws, int nw) {
+    int64_t b = 0;
+    for (int i = 0; i < nw; ++i) b += units_blocks(ws[i]);
+    return b;
+}
+
 // Shared by the stacked and batched entry points: segment i goes to outs[i].
 int dequant_segments(const nf4_weight *ws, int nw, void *const *outs, int out_dtype,
                      void *stream) {
@@ -178,9 +274,7 @@ int dequant_segments(const nf4_weight *ws, int nw, void *const *outs, int out_dt
         a.out[i] = outs[i];
         const int64_t n = ws[i].rows * ws[i].cols;
         if (n > 0 && !outs[i]) return NF4_ERR_ARG;
-        units_ok = units_ok && ws[i].blocksize >= 8 && log2_exact(ws[i].blocksize) >= 0 &&
-                   (!ws[i].nested || log2_exact(ws[i].blocksize2) >= 0) &&
-                   aligned(ws[i].packed, 4) && aligned(outs[i], 16) && n < (int64_t(1) << 32);
+        units_ok = units_ok && units_layout_ok(ws[i], outs[i]);
     }
     const int path = units_ok ? kUnits : kElements;
     // Grid: the vector path covers ceil(units (+1 partial) / (threads * unroll)) workgroups per
@@ -190,8 +284,7 @@ int dequant_segments(const nf4_weight *ws, int nw, void *const *outs, int out_dt
         const int64_t n = ws[i].rows * ws[i].cols;
         int64_t blocks;
         if (path == kUnits) {
-            const int64_t units = (n >> 3) + ((n & 7) ? 1 : 0);
-            blocks = (units + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+            blocks = units_blocks(ws[i]);
         } else {
             blocks = (n + kThreads - 1) / kThreads;
             if (blocks > 65536) blocks = 65536;
@@ -229,6 +322,76 @@ extern "C" int nf4_dequant_batch(const nf4_weight *ws, int nw, void *const *outs
     for (int i = 0; i < nw; ++i) total += ws[i].rows * ws[i].cols;
     if (total == 0) return NF4_OK;
     return dequant_segments(ws, nw, outs, out_dtype, stream);
+}
+
+
+extern "C" size_t nf4_dequant_table_bytes(const nf4_weight *ws, int nw) {
+    if (!ws || nw < 1) return 0;
+    for (int i = 0; i < nw; ++i)
+        if (ws[i].rows < 0 || ws[i].cols < 0) return 0;
+    return static_cast<size_t>(table_index_offset(nw) + table_blocks(ws, nw) * 4);
+}
+
+extern "C" int nf4_dequant_table_pack(const nf4_weight *ws, int nw, void *const *outs,
+                                      int out_dtype, void *table, size_t table_bytes,
+                                      int64_t *blocks) {
+    if (!ws || !outs || !table || !blocks || nw < 1) return NF4_ERR_ARG;
+    if (out_dtype != NF4_F16 && out_dtype != NF4_BF16 && out_dtype != NF4_F32) return NF4_ERR_ARG;
+    for (int i = 0; i < nw; ++i) {
+        const int st = check_weight(&ws[i]);
+        if (st != NF4_OK) return st;
+        if (ws[i].rows * ws[i].cols > 0 && !outs[i]) return NF4_ERR_ARG;
+        if (!units_layout_ok(ws[i], outs[i])) return NF4_ERR_UNSUPPORTED;
+    }
+    const size_t need = nf4_dequant_table_bytes(ws, nw);
+    if (table_bytes < need) return NF4_ERR_WORKSPACE;
+    const int64_t total = table_blocks(ws, nw);
+    if (total > 0x7fffffff) return NF4_ERR_UNSUPPORTED;
+    uint8_t *t = static_cast<uint8_t *>(table);
+    TableHeader h = {};
+    h.tag = kTableTag;
+    h.nw = nw;
+    h.out_dtype = out_dtype;
+    h.blocks = total;
+    h.entries = table_entries_offset();
+    h.index = table_index_offset(nw);
+    std::memset(t, 0, static_cast<size_t>(h.index));
+    std::memcpy(t, &h, sizeof(h));
+    uint32_t *index = reinterpret_cast<uint32_t *>(t + h.index);
+    int64_t b = 0;
+    for (int i = 0; i < nw; ++i) {
+        TableEntry e = {};
+        e.w = to_dev(ws[i]);
+        e.out = outs[i];
+        e.block_start = b;
+        std::memcpy(t + h.entries + static_cast<int64_t>(i) * sizeof(TableEntry), &e, sizeof(e));
+        const int64_t nbk = units_blocks(ws[i]);
+        for (int64_t j = 0; j < nbk; ++j) index[b + j] = static_cast<uint32_t>(i);
+        b += nbk;
+    }
+    *blocks = total;
+    return NF4_OK;
+}
+
+extern "C" int nf4_dequant_table(const void *table, int nw, int64_t blocks, int out_dtype,
+                                 void *stream) {
+    if (out_dtype != NF4_F16 && out_dtype != NF4_BF16 && out_dtype != NF4_F32) return NF4_ERR_ARG;
+    if (nw < 1 || blocks < 0 || blocks > 0x7fffffff || (blocks > 0 && !aligned(table, 64)))
+        return NF4_ERR_ARG;
+    if (blocks == 0) return NF4_OK;
+    const dim3 g(static_cast<unsigned>(blocks)), b(kThreads);
+    auto s = static_cast<hipStream_t>(stream);
+    const uint8_t *t = static_cast<const uint8_t *>(table);
+    const auto *h = reinterpret_cast<const TableHeader *>(t);
+    const auto *e = reinterpret_cast<const TableEntry *>(t + table_entries_offset());
+    const auto *ix = reinterpret_cast<const uint32_t *>(t + table_index_offset(nw));
+    if (out_dtype == NF4_F16)
+        hipLaunchKernelGGL(dequant_table_kernel<NF4_F16>, g, b, 0, s, h, e, ix, nw, blocks);
+    else if (out_dtype == NF4_BF16)
+        hipLaunchKernelGGL(dequant_table_kernel<NF4_BF16>, g, b, 0, s, h, e, ix, nw, blocks);
+    else
+        hipLaunchKernelGGL(dequant_table_kernel<NF4_F32>, g, b, 0, s, h, e, ix, nw, blocks);
+    return status_of(hipGetLastError());
 }
 
 extern "C" int nf4_dequant(const nf4_weight *w, void *out, int out_dtype, void *stream) {

@@ -61,6 +61,10 @@ _SIGNATURES = {
     "nf4_dequant_multi": (c_int, [ctypes.POINTER(NF4Weight), c_int, c_void_p, c_int, c_void_p]),
     "nf4_dequant_batch": (c_int, [ctypes.POINTER(NF4Weight), c_int, ctypes.POINTER(c_void_p),
                                   c_int, c_void_p]),
+    "nf4_dequant_table_bytes": (c_size_t, [ctypes.POINTER(NF4Weight), c_int]),
+    "nf4_dequant_table_pack": (c_int, [ctypes.POINTER(NF4Weight), c_int, ctypes.POINTER(c_void_p),
+                                       c_int, c_void_p, c_size_t, ctypes.POINTER(c_int64)]),
+    "nf4_dequant_table": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p]),
     "nf4_linear_fwd": (c_int, [c_void_p, c_int64, c_int64, ctypes.POINTER(NF4Weight), c_int,
                                c_void_p, ctypes.POINTER(NF4Lora), c_int, c_void_p, c_int64, c_int,
                                c_void_p, c_size_t, c_void_p]),

@@ -68,6 +68,38 @@ def dequant_batch(weights, dtype=torch.float16, outs=None) -> list:
     return outs
 
 
+class DequantTable:
+    """Any number of weights dequantized by one launch (nf4_dequant_table): the descriptor
+    table is packed once on the host and kept in device memory; `run()` launches on torch's
+    current stream.  `outs` default to fresh [rows, cols] tensors; the weights and outputs must
+    stay alive (and in place) as long as the table is used - this object keeps references."""
+
+    def __init__(self, weights, dtype=torch.float16, outs=None):
+        packed0 = weights[0][0]
+        _check_device(packed0)
+        if outs is None:
+            outs = [torch.empty(tuple(int(d) for d in qs.shape), dtype=dtype,
+                                device=packed0.device) for _, qs in weights]
+        self.weights, self.outs, self.dtype = list(weights), list(outs), dtype
+        self._code = _code(dtype, (torch.float16, torch.bfloat16, torch.float32))
+        arr = _descs(weights)
+        lib = load()
+        nbytes = lib.nf4_dequant_table_bytes(arr, len(weights))
+        host = torch.empty(max(nbytes, 16), dtype=torch.uint8)
+        ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+        blocks = ctypes.c_int64(0)
+        check(lib.nf4_dequant_table_pack(arr, len(weights), ptrs, self._code, host.data_ptr(),
+                                         nbytes, ctypes.byref(blocks)), "nf4_dequant_table_pack")
+        self.blocks = int(blocks.value)
+        self.table = host.to(packed0.device)
+        self.refs = [w for pair in weights for w in pair]
+
+    def run(self):
+        check(load().nf4_dequant_table(self.table.data_ptr(), len(self.weights), self.blocks,
+                                       self._code, stream_of(self.table)), "nf4_dequant_table")
+        return self.outs
+
+
 def _workspace(nbytes: int, device) -> torch.Tensor | None:
     if nbytes == 0:
         return None

@@ -107,3 +107,50 @@ def test_fixtures_reproduce_with_oracle():
         np.testing.assert_array_equal(o.dequantize(packed, st, "bf16"), z[f"{name}/w_bf16"])
         y = o.linear_fwd(z[f"{name}/x"], z[f"{name}/w_f16"], z[f"{name}/bias"]).numpy()
         np.testing.assert_allclose(y, z[f"{name}/y_ref"], rtol=1e-5, atol=1e-6)
+
+
+def test_dequant_table_pack_on_the_host(lib):
+    """nf4_dequant_table_pack is host code: it validates the weights (unsupported layouts,
+    a short buffer) and lays out header, entries and the per-workgroup weight index, whose
+    workgroup counts follow the 8-elements-per-thread, 256-thread, 8-unit layout."""
+    from solution._lib import NF4_ERR_UNSUPPORTED, NF4_ERR_WORKSPACE, NF4_OK, NF4Weight
+
+    buf = (ctypes.c_uint8 * 4096)()
+    code = (ctypes.c_float * 272)()
+    a = ctypes.addressof(buf)
+
+    def w(rows, cols, bs=64, nested=1):
+        return NF4Weight(packed=a, absmax=a, absmax2=ctypes.addressof(code),
+                         code2=ctypes.addressof(code), code=ctypes.addressof(code), nested=nested,
+                         rows=rows, cols=cols, blocksize=bs, blocksize2=256)
+
+    shapes = [(1536, 1536), (256, 1536), (8960, 1536), (3, 100)]
+    ws = (NF4Weight * 4)(*[w(r, c) for r, c in shapes])
+    outs = (ctypes.c_void_p * 4)(*[a + 64 * i for i in range(4)])
+    nbytes = lib.nf4_dequant_table_bytes(ws, 4)
+    per_wg = 256 * 8 * 8
+    blocks_each = [-(-(-(-r * c // 8)) // (256 * 8)) for r, c in shapes]
+    assert blocks_each[:3] == [r * c // per_wg for r, c in shapes[:3]]
+    host = (ctypes.c_uint8 * nbytes)()
+    blocks = ctypes.c_int64(0)
+    assert lib.nf4_dequant_table_pack(ws, 4, outs, 0, host, nbytes - 1,
+                                      ctypes.byref(blocks)) == NF4_ERR_WORKSPACE
+    assert lib.nf4_dequant_table_pack(ws, 4, outs, 0, host, nbytes, ctypes.byref(blocks)) == NF4_OK
+    assert blocks.value == sum(blocks_each)
+    raw = bytes(host)
+    tag, nw, dt = np.frombuffer(raw[:12], np.uint32)
+    assert (tag, nw, dt) == (0x4E463454, 4, 0)
+    hdr = np.frombuffer(raw[16:40], np.int64)
+    assert hdr[0] == blocks.value
+    index = np.frombuffer(raw[hdr[2]:hdr[2] + 4 * blocks.value], np.uint32)
+    np.testing.assert_array_equal(index, np.repeat(np.arange(4), blocks_each))
+    assert nbytes == hdr[2] + 4 * blocks.value
+    odd = (NF4Weight * 1)(w(4, 96, bs=96))  # not a power of two: the batch entry points' job
+    n1 = lib.nf4_dequant_table_bytes(odd, 1)
+    h1 = (ctypes.c_uint8 * n1)()
+    assert lib.nf4_dequant_table_pack(odd, 1, outs, 0, h1, n1,
+                                      ctypes.byref(blocks)) == NF4_ERR_UNSUPPORTED
+    misaligned = (ctypes.c_void_p * 1)(a + 8)
+    one = (NF4Weight * 1)(w(4, 64))
+    assert lib.nf4_dequant_table_pack(one, 1, misaligned, 0, h1, n1,
+                                      ctypes.byref(blocks)) == NF4_ERR_UNSUPPORTED

@@ -198,3 +198,37 @@ def test_checkpoint_loads_into_kernels(cuda, tmp_path, nested):
     w = dequantize_nf4(p2, q2, torch.float16)
     assert torch.equal(w.cpu().view(torch.int16), oracle_w16(p2, q2).view(torch.int16))
     assert torch.equal(w, dequantize_nf4(packed, qs, torch.float16))
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+def test_table_bit_exact(cuda, dt):
+    """One table launch over 21 weights (three layers' worth of shapes, nested and plain,
+    blocksizes 8 to 256, an element count that is not a multiple of 8): every output bit-exact,
+    also on a second launch into cleared outputs; a launch whose dtype or workgroup count does
+    not match the table writes nothing (a wrong weight count is refused before the launch)."""
+    from solution import kernels
+
+    banner("dequant table", dt)
+    shapes = [(192, 128, 64, True), (64, 128, 64, True), (64, 128, 64, False),
+              (128, 128, 128, True), (320, 128, 256, True), (320, 128, 8, True),
+              (128, 320, 64, True)]
+    ws = [random_weight(n, k, seed=600 + 10 * layer + i, dev=cuda, blocksize=bs, nested=nest)
+          for layer in range(3) for i, (n, k, bs, nest) in enumerate(shapes)]
+    ws.append(random_weight(3, 100, seed=699, dev=cuda))  # 300 elements: a partial unit
+    table = kernels.DequantTable(ws, DT[dt])
+    for rep in range(2):
+        for out in table.outs:
+            out.zero_()
+        table.run()
+        for (p, qs), out in zip(ws, table.outs):
+            assert torch.equal(_bits(out).reshape(-1), _oracle(p, qs, dt).reshape(-1)), rep
+    for out in table.outs:
+        out.zero_()
+    lib, s = kernels.load(), kernels.stream_of(table.table)
+    other = 1 if dt == "f16" else 0
+    nw = len(ws)
+    assert lib.nf4_dequant_table(table.table.data_ptr(), nw, table.blocks, other, s) == 0
+    assert lib.nf4_dequant_table(table.table.data_ptr(), nw, table.blocks - 1, table._code, s) == 0
+    torch.cuda.synchronize()
+    assert all(not out.any() for out in table.outs)
+    assert lib.nf4_dequant_table(table.table.data_ptr(), 0, table.blocks, table._code, s) != 0
