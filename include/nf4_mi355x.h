@@ -144,6 +144,22 @@ int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy,
                   void *workspace, size_t workspace_bytes, void *stream);
 size_t nf4_linear_dx_workspace(int64_t m, const nf4_weight *ws, int nw, int dtype);
 
+/* nf4_linear_dx without a workspace argument: it allocates nothing, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).  No counterpart in the reference.  Split-K partials go to one static
+ * device array of NF4_STATIC_SCRATCH_BYTES per GPU, set up when the library's code loads on a
+ * device and held until the process ends; its address is looked up on the first call on each
+ * device (make that first call outside graph capture).  The tiling is nf4_linear_dx's, chosen
+ * among the plans whose partials fit the array (plans with no split need none), so every size
+ * is accepted; the result equals nf4_linear_dx's bit for bit whenever its plan fits.  The
+ * array keeps the last call's partials; calls that overlap on one GPU (other streams or
+ * threads) share it and race.  The stream must belong to the current device. */
+#define NF4_STATIC_SCRATCH_BYTES (64u << 20)
+int nf4_linear_dx_noalloc(const void *dy, int64_t m, int64_t lddy,
+                          const nf4_weight *ws, int nw,
+                          const nf4_lora *loras, int nlora,
+                          void *dx, int64_t lddx, int accumulate, int dtype, void *stream);
+
 /* The same two GEMMs with the tiling pinned instead of chosen by the library's cost model:
  * tile NF4_TILE_256 (256x256 tiles, 8 waves), NF4_TILE_128 (128x128, 4 waves) or
  * NF4_TILE_128_KSPLIT2 (128x128, two groups of 4 waves splitting each tile's reduction), with

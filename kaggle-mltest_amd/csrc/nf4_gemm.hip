@@ -31,6 +31,8 @@
 // Long reductions are split over workgroups into fp32 partial sums that a reduction kernel
 // adds up in a fixed order (deterministic).
 
+#include <mutex>
+
 #include "nf4_common.h"
 
 namespace {
@@ -1540,17 +1542,24 @@ double plan_cost(int cfg, int64_t tiles, int64_t mt, int64_t tail_start, int spl
     return c + split_cost;
 }
 
-Plan make_plan(int64_t m, int64_t big, int64_t small, int64_t steps, int max_splits = kMaxSplits) {
+// `ws_cap` >= 0 (input-gradient plans only, `out_cols` = K): leave out split plans whose fp32
+// partials, splits x M x (columns from the tail's first p tile to K), exceed ws_cap bytes.
+Plan make_plan(int64_t m, int64_t big, int64_t small, int64_t steps, int max_splits = kMaxSplits,
+               int64_t out_cols = 0, int64_t ws_cap = -1) {
     Plan best{};
     double best_cost = 0.0;
     for (int cfg : {0, 1, 3}) {
         const int64_t tiles = cfg == 0 ? big : small;
         const int64_t mt = (m + (cfg == 0 ? 255 : 127)) / (cfg == 0 ? 256 : 128);
+        const int64_t bp = cfg == 0 ? 256 : 128;
         for (int s = 1; s <= max_splits; ++s) {
             const int64_t per = (steps + s - 1) / s;
             if (s > 1 && (s - 1) * per >= steps) break;  // no empty split
             // the split tail starts at a p-tile boundary (a column range of the output)
             for (int64_t ts = 0; ts < (s > 1 ? tiles : 1); ts += mt) {
+                if (s > 1 && ws_cap >= 0 &&
+                    int64_t(s) * m * (out_cols - (ts / mt) * bp) * 4 > ws_cap)
+                    continue;
                 const double c = plan_cost(cfg, tiles, mt, ts, s, steps, m);
                 if (best.splits == 0 || c < best_cost) {
                     best = Plan{cfg, cfg == 0 ? 256 : 128, cfg == 0 ? 256 : 128, s, tiles, 0,
@@ -1649,14 +1658,15 @@ Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits
     return make_plan(m, big, small, ws[0].cols / BR);
 }
 
-Plan plan_dx(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1) {
+Plan plan_dx(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1,
+             int64_t ws_cap = -1) {
     int64_t steps = 0;
     for (int i = 0; i < nw; ++i) steps += (ws[i].rows + BR - 1) / BR;
     const int64_t K = ws[0].cols;
     const int64_t big = ((K + 255) / 256) * ((m + 255) / 256);
     const int64_t small = ((K + 127) / 128) * ((m + 127) / 128);
     if (tile >= 0) return pinned_plan(tile, splits, big, small, steps);
-    return make_plan(m, big, small, steps);
+    return make_plan(m, big, small, steps, kMaxSplits, K, ws_cap);
 }
 
 template <int DT>
@@ -1882,10 +1892,14 @@ extern "C" int nf4_linear_fwd(const void *x, int64_t m, int64_t ldx, const nf4_w
                                 workspace_bytes, stream, NF4_TILE_AUTO, 1);
 }
 
-extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws,
-                                   int nw, const nf4_lora *loras, int nlora, void *dx,
-                                   int64_t lddx, int accumulate, int dtype, void *workspace,
-                                   size_t workspace_bytes, void *stream, int tile, int splits) {
+namespace {
+
+// nf4_linear_dx_tiled with the automatic plan restricted to split-K partials of at most
+// ws_cap bytes (ws_cap < 0: no restriction).
+int linear_dx_impl(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws, int nw,
+                   const nf4_lora *loras, int nlora, void *dx, int64_t lddx, int accumulate,
+                   int dtype, void *workspace, size_t workspace_bytes, void *stream, int tile,
+                   int splits, int64_t ws_cap) {
     if (dtype != NF4_F16 && dtype != NF4_BF16) return NF4_ERR_ARG;
     if (m < 0 || !dx || (m > 0 && !dy) || nlora < 0 || (nlora > 0 && !loras)) return NF4_ERR_ARG;
     GemmArgs g;
@@ -1917,7 +1931,7 @@ extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, cons
     g.n_out = g.K;
     g.accumulate = accumulate != 0;
     g.vec_out = aligned(dx, 8) && lddx % 4 == 0;
-    const Plan p = plan_dx(m, ws, nw, tile, splits);
+    const Plan p = plan_dx(m, ws, nw, tile, splits, ws_cap);
     if (p.splits == 0) return NF4_ERR_ARG;
     g.splits = p.splits;
     const int64_t bp = p.bp, bm = p.bm;
@@ -1949,12 +1963,68 @@ extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, cons
                              : launch_reduce<NF4_F16>(g, p.splits, s);
 }
 
+// ------------------------------------------------- the allocation-free input gradient
+//
+// nf4_linear_dx_noalloc keeps its split-K partials in `scratch`, one array of
+// NF4_STATIC_SCRATCH_BYTES per GPU, allocated when the library's code is loaded on a device
+// and held until the process ends.  In host code `scratch` names a host-side stand-in, not
+// device memory: its device address is looked up once per device (hipGetSymbolAddress, with
+// that device current, on the entry point's first call there) and only that address is used.
+// Every split tile writes all of its partials before the reduction reads them, so nothing in
+// the array needs clearing between calls.  Calls that overlap on one GPU (two streams, two
+// threads) share the array and race.
+
+static __device__ __align__(256) uint8_t scratch[NF4_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on the current device.
+int scratch_on_current_device(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return NF4_ERR_LAUNCH;
+    if (dev < 0 || dev >= kMaxScratchDevices) return NF4_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+            return NF4_ERR_LAUNCH;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return NF4_OK;
+}
+
+}  // namespace
+
+extern "C" int nf4_linear_dx_tiled(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws,
+                                   int nw, const nf4_lora *loras, int nlora, void *dx,
+                                   int64_t lddx, int accumulate, int dtype, void *workspace,
+                                   size_t workspace_bytes, void *stream, int tile, int splits) {
+    return linear_dx_impl(dy, m, lddy, ws, nw, loras, nlora, dx, lddx, accumulate, dtype,
+                          workspace, workspace_bytes, stream, tile, splits, -1);
+}
+
 extern "C" int nf4_linear_dx(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws, int nw,
                              const nf4_lora *loras, int nlora, void *dx, int64_t lddx,
                              int accumulate, int dtype, void *workspace, size_t workspace_bytes,
                              void *stream) {
-    return nf4_linear_dx_tiled(dy, m, lddy, ws, nw, loras, nlora, dx, lddx, accumulate, dtype,
-                               workspace, workspace_bytes, stream, NF4_TILE_AUTO, 1);
+    return linear_dx_impl(dy, m, lddy, ws, nw, loras, nlora, dx, lddx, accumulate, dtype,
+                          workspace, workspace_bytes, stream, NF4_TILE_AUTO, 1, -1);
+}
+
+extern "C" int nf4_linear_dx_noalloc(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws,
+                                     int nw, const nf4_lora *loras, int nlora, void *dx,
+                                     int64_t lddx, int accumulate, int dtype, void *stream) {
+    void *ws_dev = nullptr;
+    const int st = scratch_on_current_device(&ws_dev);
+    if (st != NF4_OK) return st;
+    // plans needing more than the array are never chosen; linear_dx_impl still checks the
+    // chosen plan's need against the size passed (NF4_ERR_WORKSPACE)
+    return linear_dx_impl(dy, m, lddy, ws, nw, loras, nlora, dx, lddx, accumulate, dtype, ws_dev,
+                          NF4_STATIC_SCRATCH_BYTES, stream, NF4_TILE_AUTO, 1,
+                          static_cast<int64_t>(NF4_STATIC_SCRATCH_BYTES));
 }
 
 namespace {

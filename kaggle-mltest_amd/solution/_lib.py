@@ -73,6 +73,9 @@ _SIGNATURES = {
                               ctypes.POINTER(NF4Lora), c_int, c_void_p, c_int64, c_int, c_int,
                               c_void_p, c_size_t, c_void_p]),
     "nf4_linear_dx_workspace": (c_size_t, [c_int64, ctypes.POINTER(NF4Weight), c_int, c_int]),
+    "nf4_linear_dx_noalloc": (c_int, [c_void_p, c_int64, c_int64, ctypes.POINTER(NF4Weight),
+                                      c_int, ctypes.POINTER(NF4Lora), c_int, c_void_p, c_int64,
+                                      c_int, c_int, c_void_p]),
     "nf4_linear_fwd_tiled": (c_int, [c_void_p, c_int64, c_int64, ctypes.POINTER(NF4Weight), c_int,
                                      c_void_p, ctypes.POINTER(NF4Lora), c_int, c_void_p, c_int64,
                                      c_int, c_void_p, c_size_t, c_void_p, c_int, c_int]),
