@@ -98,6 +98,8 @@ struct GemmArgs {
     int vec_out;                  // 8-byte output stores allowed (paired: and aux loads)
     const uint16_t *aux;          // paired SwiGLU backward: dH [M, I]
     int64_t ld_aux;
+    int rows_groups;              // row-streaming path: row groups per workgroup
+    int rows_parts;               // row-streaming path: K parts per row
 };
 
 template <int DT>
@@ -1229,6 +1231,249 @@ void gemv_kernel(const GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------- row-streaming decode path
+//
+// Y = X W^T for M <= 2 tokens: bound by reading the packed weight once.  A row is cut into 1 KB
+// slots of packed bytes (2048 k; lane l of a wave takes the 16 bytes at 16 l, 32 elements inside
+// one absmax block) and the slots into K parts of SP <= 2 slots.  A wave owns one K part of up
+// to kRowsMaxRows consecutive rows of one segment and keeps its part's activations (64 bytes per
+// lane, slot and token) in registers for all of them, so the main loop streams weight bytes
+// only.  A constant 256-entry LDS table maps a packed byte to its two codes rounded to the GEMM
+// dtype as one pair (code[high nibble] in the low half: element order): a packed byte is one
+// table read and, per token, one v_dot2 with the activation pair, accumulated in fp32, and a
+// lane's 32 products are then scaled by their block's fp32 absmax (rebuilt as in the other
+// kernels).  The numerics are those of bitsandbytes' decode GEMV (no fp16 weight is formed)
+// except that the 16 codes are rounded to the GEMM dtype: each product is round16(code[nib]) * x
+// exactly and a block's sum is scaled by its absmax in fp32.
+//
+// After each row the lane partials are reduced across the wave in a fixed order (DPP within
+// rows of 16 lanes, then the four rows) and lane r keeps the sum of the wave's row r.  Rows with
+// several K parts (K > SP x 2048) are shared by the waves of one workgroup, which add their
+// parts through LDS in part order after the loop: deterministic.  The LoRA term of a row (lanes
+// < rank; the B row is loaded with the row's weight bytes) joins the first part's partial before
+// the reduction, the bias is added at the store.  Lanes past a row's end, and slots of a part
+// past it, multiply activations that read as zero (their resource ends with the activation
+// row), so the loop has no masks; the weight bytes they read belong to the next row or read as
+// zero past the weight.  Each wave keeps kRowsRing rows of loads in flight (measured: deeper
+// rings were slower), re-reading its last row past its range rather than branching.
+constexpr int64_t kRowsMaxM = 2;
+constexpr int kRowsMaxParts = 8;    // K <= 8 x 2 x 2048
+constexpr int kRowsMaxRows = 64;    // rows per wave: one result lane each
+constexpr int kRowsMaxWaves = 16;
+constexpr int kRowsRing = 2;        // rows of loads in flight per wave
+
+// The map `a.map[0]`: tile_start[s] = first row group of segment s (cumulative), m_tiles = rows
+// per group; a workgroup runs a.rows_groups groups x a.rows_parts K parts, wave w taking part
+// w % rows_parts of group w / rows_parts.
+// (4 waves per SIMD are enough: squeezed for more, the compiler reuses registers that loads
+// in flight still target, which waits for them.)
+template <int DT, int MT, int SP>
+__global__ __launch_bounds__(kRowsMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void gemv_rows_kernel(const GemmArgs a) {
+    constexpr int RD = kRowsRing;
+    __shared__ uint32_t s_pair[kMaxSeg][256];
+    __shared__ float s_code2[kMaxSeg][256];
+    __shared__ float s_part[kRowsMaxWaves][MT][64];
+    const int np = a.rows_parts;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int part = wave % np;
+    const int64_t grp = static_cast<int64_t>(blockIdx.x) * a.rows_groups + wave / np;
+    const TileMap &tm = a.map[0];
+    const bool active = grp < tm.tile_start[a.nseg];
+    const int seg = active ? seg_of_tile(a, tm, grp) : 0;
+    const DevWeight w = a.w[seg];
+    const int64_t row0 = uniform64(active ? (grp - tm.tile_start[seg]) * tm.m_tiles : 0);
+    const int nrows = active ? static_cast<int>(tm.m_tiles < w.rows - row0 ? tm.m_tiles : w.rows - row0) : 0;
+    const int64_t K = a.K;
+    const int khalf = static_cast<int>(K / 2);
+    const int lane = threadIdx.x & 63;
+    const int slot0 = part * SP;
+    const WeightRsrc wr = weight_rsrc(w);
+    const LoraDev lo = a.lora[seg];
+    const bool lora = lo.has && part == 0;
+    const float lscale = lora ? lo.scale : 0.0f;
+    // Byte and 16-bit operands are loaded as the aligned dwords that hold them and picked out at
+    // use: a loop-carried sub-dword load gets a zero-extension at the loop's back edge, which
+    // waits for it.  The dword of the last byte may extend past the operand (the host checks
+    // that both bases are 4-byte aligned, so it never crosses a page).
+    const rsrc_t br = make_rsrc(lo.b, lora ? (w.rows * lo.rank * 2 + 3) & ~int64_t(3) : 0);
+    const int64_t nblk = (w.rows * w.cols + w.blocksize - 1) >> w.bs_shift;
+    const rsrc_t qr = make_rsrc(w.absmax, w.nested ? (nblk + 3) & ~int64_t(3) : 0);
+    const int kb = static_cast<int>(K >> w.bs_shift);  // absmax blocks per row
+    const int qbase = static_cast<int>(row0) * kb;
+
+    // The tables: thread i < 256 (every workgroup has at least 512 threads) writes entry i of
+    // each segment's tables after the barrier below.  Their loads go first, from every thread
+    // (a branch here would leave them in flight behind the ring loads on some paths, which
+    // makes the loop's wait counts conservative).
+    const int i = threadIdx.x & 255;
+    uint32_t hi[kMaxSeg], lo2[kMaxSeg], c2[kMaxSeg];
+#pragma unroll
+    for (int s = 0; s < kMaxSeg; ++s) {
+        const rsrc_t cr = make_rsrc(a.w[s].code, s < a.nseg ? 64 : 0);
+        const rsrc_t c2r = make_rsrc(a.w[s].code2, s < a.nseg && a.w[s].nested ? 1024 : 0);
+        hi[s] = bload4(cr, (i >> 4) * 4);
+        lo2[s] = bload4(cr, (i & 15) * 4);
+        c2[s] = bload4(c2r, i * 4);
+    }
+    // LoRA T[m][lane] (dword loads, like the B rows below: no wait here)
+    const rsrc_t tr = make_rsrc(lo.t, lora ? (a.M * lo.rank * 2 + 3) & ~int64_t(3) : 0);
+    uint32_t tw[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) tw[m] = bload4(tr, (m * lo.rank + lane) * 2 & ~3);
+    // this part's activations: token m, slot s holds elements 2048 (slot0 + s) + 32 lane .. + 31
+    u32x4_t xr[SP][MT][4];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const rsrc_t xs = make_rsrc(a.act + m * a.ld_act, m < a.M ? K * 2 : 0);
+#pragma unroll
+        for (int sl = 0; sl < SP; ++sl)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xr[sl][m][q] = bload16(xs, (slot0 + sl) * 4096 + lane * 64 + q * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the ring loads below stay behind these
+
+    struct Slot {
+        u32x4_t p;
+        uint32_t qw;  // dword holding the block's uint8 absmax code (nested)
+        float s;      // absmax2 scale (nested) or the fp32 absmax
+    };
+    Slot ring[RD][SP];
+    uint32_t lbw[RD];  // dword holding the row's LoRA B value of this lane
+    int lblk[SP];      // absmax block of this lane's bytes in a slot, relative to the row
+#pragma unroll
+    for (int sl = 0; sl < SP; ++sl) lblk[sl] = (2 * (1024 * (slot0 + sl) + 16 * lane)) >> w.bs_shift;
+    const int last = nrows > 0 ? nrows - 1 : 0;  // an inactive wave re-reads row 0 of segment 0
+    auto load = [&](int j, int r) {
+        const int rr = r < nrows ? r : last;
+        const int64_t row = row0 + rr;
+#pragma unroll
+        for (int sl = 0; sl < SP; ++sl) {
+            const int byte = 1024 * (slot0 + sl) + 16 * lane;
+            const int b = qbase + rr * kb + lblk[sl];
+            ring[j][sl].p = bload16(wr.packed, static_cast<int>(row * khalf) + byte);
+            ring[j][sl].qw = bload4(qr, b & ~3);
+            ring[j][sl].s = __builtin_bit_cast(float, bload4(wr.s, (wr.nested ? b >> wr.bs2_shift : b) * 4));
+        }
+        lbw[j] = bload4(br, (static_cast<int>(row) * lo.rank + lane) * 2 & ~3);
+    };
+    // The first rows' loads go out before the table work, so their latency overlaps it; issued
+    // by every wave (an inactive one reads row 0), so that the wait below retires the
+    // activation loads on every path.
+    // Row by row, in the loop's order (interleaved, the loop's wait counts inherit the worst
+    // position a row's loads had here).
+#pragma unroll
+    for (int j = 0; j < RD; ++j) {
+        load(j, j);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    if (threadIdx.x < 256) {  // write the tables (loaded at the top)
+#pragma unroll
+        for (int s = 0; s < kMaxSeg; ++s) {
+            if (s >= a.nseg) break;
+            s_pair[s][i] = static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, hi[s]))) |
+                           (static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, lo2[s]))) << 16);
+            s_code2[s][i] = a.w[s].nested ? __builtin_bit_cast(float, c2[s]) : (i == 0 ? 1.0f : 0.0f);
+        }
+    }
+    __syncthreads();
+
+    // Retire the activation loads (all but the ring's RD rows of loads, issued after them)
+    // before the loop: left in flight into it, they make the compiler's wait counts for the
+    // ring loads conservative down to zero.
+    constexpr int kRingLoads = RD * (3 * SP + 1);
+    static_assert(kRingLoads < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((kRingLoads & 0xF) | ((kRingLoads >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+    float tv[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const uint16_t h = static_cast<uint16_t>(tw[m] >> (((m * lo.rank + lane) & 1) * 16));
+        tv[m] = (lane < lo.rank && m < a.M) ? to_f32<DT>(h) : 0.0f;
+    }
+    float res[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) res[m] = 0.0f;
+    const uint32_t *pair = s_pair[seg];
+    const float *code2 = s_code2[seg];
+    // Whole rounds of RD rows; the ring slot of a row past the range (a re-read of the last
+    // row) is refilled but not computed.
+    for (int r0 = 0; r0 < nrows; r0 += RD) {
+#pragma unroll
+        for (int j = 0; j < RD; ++j) {
+            const int r = r0 + j;
+            const int rr = r < nrows ? r : last;  // the row the ring holds
+            if (r < nrows) {
+            float acc[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+#pragma unroll
+            for (int sl = 0; sl < SP; ++sl) {
+                const Slot &sv = ring[j][sl];
+                const int sh = ((qbase + rr * kb + lblk[sl]) & 3) * 8;
+                const float sc = absmax_val(w, AbsIn{sv.s, (sv.qw >> sh) & 0xFFu}, code2);
+                const uint32_t pw[4] = {sv.p.x, sv.p.y, sv.p.z, sv.p.w};
+                uint32_t t[16];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    t[4 * d + 0] = pair[pw[d] & 0xFF];
+                    t[4 * d + 1] = pair[(pw[d] >> 8) & 0xFF];
+                    t[4 * d + 2] = pair[(pw[d] >> 16) & 0xFF];
+                    t[4 * d + 3] = pair[pw[d] >> 24];
+                }
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const u32x4_t xq = xr[sl][m][q];
+                        d0 = dot2<DT>(t[4 * q + 0], xq.x, d0);
+                        d1 = dot2<DT>(t[4 * q + 1], xq.y, d1);
+                        d0 = dot2<DT>(t[4 * q + 2], xq.z, d0);
+                        d1 = dot2<DT>(t[4 * q + 3], xq.w, d1);
+                    }
+                    acc[m] += (d0 + d1) * sc;
+                }
+            }
+            {  // LoRA (branch-free: tv is zero without it, and lbw reads zero)
+                const int e = static_cast<int>(row0 + rr) * lo.rank + lane;
+                const float bv = to_f32<DT>(static_cast<uint16_t>(lbw[j] >> ((e & 1) * 16)));
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[m] += lscale * (tv[m] * bv);
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const float tot = wave_sum(acc[m]);
+                res[m] = lane == r ? tot : res[m];
+            }
+            }
+            // The refill of ring slot j stays after the code that reads it and before the next
+            // row's: hoisted, it needs copies of the slot that wait for every load in flight.
+            __builtin_amdgcn_sched_barrier(0);
+            load(j, r + RD);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    if (np > 1) {  // add the other parts' sums, in part order, into part 0's
+#pragma unroll
+        for (int m = 0; m < MT; ++m) s_part[wave][m][lane] = res[m];
+        __syncthreads();
+        if (part == 0) {
+            for (int p = 1; p < np; ++p)
+#pragma unroll
+                for (int m = 0; m < MT; ++m) res[m] += s_part[wave + p][m][lane];
+        }
+    }
+    if (part == 0 && lane < nrows) {
+        const int64_t col = a.seg_off[seg] + row0 + lane;
+        const float bias = a.bias ? to_f32<DT>(a.bias[col]) : 0.0f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            if (m < a.M) static_cast<uint16_t *>(a.out)[m * a.ld_out + col] = round16<DT>(res[m] + bias);
+    }
+}
+
 // One workgroup of the input-gradient GEMM (as fwd_body).
 template <int DT, int BP, int BM, int WP, int WM, int KG>
 __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, uint32_t blk,
@@ -1449,6 +1694,7 @@ struct Plan {
     // of the stacked weights forward, columns of dX backward), then the rest in unsplit 128x128
     // tiles of tiling `cfg` (1 or 3); `tiles` then counts the second launch's tiles (estimate).
     int64_t head_ptiles;
+    int rows_g = 0;  // row-streaming path: row groups per workgroup
 
     int64_t blocks() const { return tail_start + (tiles - tail_start) * splits; }
 };
@@ -1640,7 +1886,48 @@ Plan pinned_plan(int tile, int splits, int64_t big, int64_t small, int64_t steps
     return Plan{tile, b, b, splits, tiles, 0, splits > 1 ? 0 : tiles};
 }
 
-Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1) {
+// Row-streaming path (M <= 2): K parts of two 1 KB slots (one when a row fits in one slot),
+// workgroups of G row groups x np parts (at most 16 waves), and the fewest rows per group that
+// still fit the launch in one round of workgroups at 4 waves per SIMD (at most 64: one result
+// lane each).  Plan::tiles counts row groups, Plan::waves holds the rows per group, Plan::bp the
+// slots per part, Plan::bm the tokens per wave (1 or 2), Plan::splits the parts and
+// Plan::rows_g the groups per workgroup.  From 3 tokens on the decode kernel's MFMA path is
+// faster (its dequant is shared by the tokens).
+Plan plan_rows(int64_t m, const nf4_weight *ws, int nw) {
+    const int mt = m <= 1 ? 1 : 2;
+    const int64_t ni = (ws[0].cols / 2 + 1023) / 1024;
+    const int sp = ni == 1 ? 1 : 2;
+    const int np = static_cast<int>((ni + sp - 1) / sp);
+    const int groups_per_wg = np == 1 ? 8 : kRowsMaxWaves / np;
+    const int wg_per_cu = kRowsMaxWaves / (np * groups_per_wg) > 1 ? kRowsMaxWaves / (np * groups_per_wg) : 1;
+    int64_t rows = 0;
+    for (int i = 0; i < nw; ++i) rows += ws[i].rows;
+    const int64_t slots = static_cast<int64_t>(kCUs) * wg_per_cu * groups_per_wg;
+    int64_t rpw = (rows + slots - 1) / slots;
+    if (rpw < 1) rpw = 1;
+    if (rpw > kRowsMaxRows) rpw = kRowsMaxRows;
+    int64_t groups = 0;
+    for (int i = 0; i < nw; ++i) groups += (ws[i].rows + rpw - 1) / rpw;
+    Plan p{6, sp, mt, np, groups, static_cast<int>(rpw), 0, 0};
+    p.rows_g = groups_per_wg;
+    return p;
+}
+
+bool rows_ok(int64_t m, const nf4_weight *ws, int nw) {
+    const int64_t ni = (ws[0].cols / 2 + 1023) / 1024;
+    if (m > kRowsMaxM || ni > 2 * kRowsMaxParts) return false;
+    for (int i = 0; i < nw; ++i)
+        if (!aligned(ws[i].absmax, 4)) return false;  // absmax codes are read as aligned dwords
+    // 32-bit byte offsets: a wave reads up to 16 KB past the start of its last row
+    for (int i = 0; i < nw; ++i)
+        if (ws[i].rows * (ws[i].cols / 2) + 16 * 1024 >= (int64_t(1) << 31)) return false;
+    return true;
+}
+
+// rows_allowed: the row-streaming path's operand alignment holds (LoRA T and B read as dwords).
+Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1,
+              bool rows_allowed = true) {
+    if (tile < 0 && rows_allowed && rows_ok(m, ws, nw)) return plan_rows(m, ws, nw);
     if (tile < 0 && m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
     if (tile < 0 && m <= kGemvMaxM) {
         int64_t n = 0;
@@ -1849,8 +2136,35 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
     g.n_out = n_out;
     g.vec_out = aligned(y, 8) && ldy % 4 == 0;
     for (int i = 0; i < nw; ++i) g.vec_out = g.vec_out && (g.seg_off[i] % 4 == 0);
-    const Plan p = plan_fwd(m, ws, nw, tile, splits);
+    bool lora_aligned = true;
+    for (int i = 0; i < nlora; ++i)
+        lora_aligned = lora_aligned && aligned(loras[i].b, 4) && aligned(loras[i].t, 4);
+    const Plan p = plan_fwd(m, ws, nw, tile, splits, lora_aligned);
     if (p.splits == 0) return NF4_ERR_ARG;
+    if (p.cfg == 6) {  // row streaming: row groups per segment, K parts per row
+        g.splits = 1;
+        g.rows_groups = p.rows_g;
+        g.rows_parts = p.splits;
+        g.map[0].m_tiles = p.waves;
+        g.map[0].tile_start[0] = 0;
+        for (int i = 0; i < nw; ++i)
+            g.map[0].tile_start[i + 1] = g.map[0].tile_start[i] + (ws[i].rows + p.waves - 1) / p.waves;
+        const dim3 grid(static_cast<unsigned>((p.tiles + p.rows_g - 1) / p.rows_g));
+        const dim3 block(p.rows_g * p.splits * 64);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (dtype == NF4_BF16) {
+            if (p.bm == 1 && p.bp == 1) hipLaunchKernelGGL((gemv_rows_kernel<NF4_BF16, 1, 1>), grid, block, 0, s, g);
+            else if (p.bm == 1) hipLaunchKernelGGL((gemv_rows_kernel<NF4_BF16, 1, 2>), grid, block, 0, s, g);
+            else if (p.bp == 1) hipLaunchKernelGGL((gemv_rows_kernel<NF4_BF16, 2, 1>), grid, block, 0, s, g);
+            else hipLaunchKernelGGL((gemv_rows_kernel<NF4_BF16, 2, 2>), grid, block, 0, s, g);
+        } else {
+            if (p.bm == 1 && p.bp == 1) hipLaunchKernelGGL((gemv_rows_kernel<NF4_F16, 1, 1>), grid, block, 0, s, g);
+            else if (p.bm == 1) hipLaunchKernelGGL((gemv_rows_kernel<NF4_F16, 1, 2>), grid, block, 0, s, g);
+            else if (p.bp == 1) hipLaunchKernelGGL((gemv_rows_kernel<NF4_F16, 2, 1>), grid, block, 0, s, g);
+            else hipLaunchKernelGGL((gemv_rows_kernel<NF4_F16, 2, 2>), grid, block, 0, s, g);
+        }
+        return status_of(hipGetLastError());
+    }
     g.splits = p.splits;
     g.per_split = (g.K / BR + p.splits - 1) / p.splits;
     const int64_t bp = p.bp, bm = p.bm;

@@ -133,6 +133,49 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jo
     }
 }
 
+// Decode-size xa (M <= kRowvecMaxM tokens): out[m][j] = scale * sum_k act[m][k] A[j][k] with one
+// workgroup per (job, row j of A) over the whole reduction, instead of one workgroup per job:
+// each of 256 threads takes 8 consecutive k per 2048-wide step (16-byte loads of the A row and
+// of every token's activations), accumulates with v_dot2 in fp32, and the workgroup adds its
+// lanes in a fixed order (DPP inside each wave, then the four waves in order).  Needs 16-byte
+// aligned rows (Job::vec == 3).
+constexpr int64_t kRowvecMaxM = 8;
+
+template <int DT, int MT>
+__global__ __launch_bounds__(256) void rowvec_kernel(const Jobs jobs, int64_t m) {
+    __shared__ float red[4][MT];
+    const Job &jb = jobs.j[blockIdx.y];
+    const int64_t k = jb.cols, ld = jb.ld;
+    const int rank = static_cast<int>(gridDim.x);
+    const int j = blockIdx.x;
+    const uint16_t *w = jb.w + j * k;
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+#pragma unroll 2
+    for (int64_t k0 = threadIdx.x * 8; k0 < k; k0 += 256 * 8) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t *>(w + k0);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            if (t >= m) break;
+            const u32x4_t x = *reinterpret_cast<const u32x4_t *>(jb.in + t * ld + k0);
+            acc[t] = dot2<DT>(a.w, x.w, dot2<DT>(a.z, x.z, dot2<DT>(a.y, x.y, dot2<DT>(a.x, x.x, acc[t]))));
+        }
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const float v = wave_sum(acc[t]);
+        if (lane == 0) red[wave][t] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < MT && threadIdx.x < m) {
+        const int t = threadIdx.x;
+        const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+        static_cast<uint16_t *>(jb.out)[t * rank + j] = st1<DT>(v * jb.scale);
+    }
+}
+
 // Partial sums over a chunk of rows on v_mfma_f32_16x16x32:
 //   part[chunk][p][j] = sum_{m in chunk} U[m][p] * V[m][j]
 // for a 64-column tile of p (4 waves x 16) and one 16-wide tile of j (blockIdx.z).  Both
@@ -371,8 +414,28 @@ int rowdot_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int d
         j.vec = (j.ld % 8 == 0 && aligned(j.in, 16) ? 1 : 0) |
                 (!B_LAYOUT && j.cols % 8 == 0 && aligned(j.w, 16) ? 2 : 0);
     }
-    const dim3 grid(static_cast<unsigned>((m + 15) / 16), static_cast<unsigned>(njobs));
     auto s = static_cast<hipStream_t>(stream);
+    bool vec = true;
+    for (int i = 0; i < njobs; ++i) vec = vec && J.j[i].vec == 3;
+    if (!B_LAYOUT && vec && m <= kRowvecMaxM) {
+        const dim3 grid(static_cast<unsigned>(rank), static_cast<unsigned>(njobs));
+        const int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+#define NF4_ROWVEC(DT, MT) hipLaunchKernelGGL((rowvec_kernel<DT, MT>), grid, dim3(256), 0, s, J, m)
+        if (dtype == NF4_BF16) {
+            if (mt == 1) NF4_ROWVEC(NF4_BF16, 1);
+            else if (mt == 2) NF4_ROWVEC(NF4_BF16, 2);
+            else if (mt == 4) NF4_ROWVEC(NF4_BF16, 4);
+            else NF4_ROWVEC(NF4_BF16, 8);
+        } else {
+            if (mt == 1) NF4_ROWVEC(NF4_F16, 1);
+            else if (mt == 2) NF4_ROWVEC(NF4_F16, 2);
+            else if (mt == 4) NF4_ROWVEC(NF4_F16, 4);
+            else NF4_ROWVEC(NF4_F16, 8);
+        }
+#undef NF4_ROWVEC
+        return status_of(hipGetLastError());
+    }
+    const dim3 grid(static_cast<unsigned>((m + 15) / 16), static_cast<unsigned>(njobs));
     if (dtype == NF4_BF16)
         hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, B_LAYOUT>), grid, dim3(kRowdotWaves * 64), 0,
                            s, J, m, rank);

@@ -248,6 +248,33 @@ def dequantize(packed: np.ndarray, state: OracleQuantState, dtype: str = "f16") 
     raise ValueError(dtype)
 
 
+def _round_to(v: np.ndarray, dtype: str) -> np.ndarray:
+    """fp32 values rounded (RNE) to ``dtype`` and returned as fp32."""
+    v = np.asarray(v, dtype=np.float32)
+    if dtype == "f16":
+        return v.astype(np.float16).astype(np.float32)
+    bits = f32_to_bf16_bits(v).astype(np.uint32) << 16
+    return bits.view(np.float32)
+
+
+def dequantize_scaled_codes(packed: np.ndarray, state: OracleQuantState,
+                            dtype: str = "f16") -> np.ndarray:
+    """The weight as the small-M (decode) GEMV multiplies it: the 16 codes rounded to the GEMM
+    dtype, each times its block's fp32 absmax in fp32, rounded once to ``dtype`` - what a
+    one-hot activation row returns.  Returns float16, or bf16 bits as uint16.  It differs
+    from ``dequantize`` (one rounding of the fp32 product code * absmax) only where the code
+    itself is not exact in ``dtype``; bitsandbytes' own decode GEMV forms no rounded weight at
+    all (fp32 code * fp32 absmax * x)."""
+    n = int(np.prod(state.shape))
+    a = absmax_fp32(state)
+    nib = nibbles(packed, n)
+    code = _round_to(state.code.astype(np.float32), dtype)
+    v = (code[nib] * a[np.arange(n) // state.blocksize]).astype(np.float32)
+    if dtype == "f16":
+        return v.astype(np.float16).reshape(state.shape)
+    return f32_to_bf16_bits(v).reshape(state.shape)
+
+
 def dequantize_loop(packed: np.ndarray, state: OracleQuantState) -> np.ndarray:
     """Element-by-element restatement (tiny inputs only): fp16 output."""
     n = int(np.prod(state.shape))

@@ -224,6 +224,26 @@ def test_small_m_stacked_bias_lora(cuda, m, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,k,r", [(1, 3584, 16), (2, 1536, 16), (5, 2056, 8), (8, 4096, 16),
+                                   (9, 1536, 16)])
+def test_lora_xa_decode_sizes(cuda, dtype, m, k, r):
+    """t = x A^T at decode token counts (up to 8 tokens: one workgroup per (adapter, A row);
+    9 tokens: the MFMA kernel), two adapters in one launch, against an fp32 product; K not a
+    multiple of the 2048-wide step."""
+    from solution import kernels
+
+    banner("lora xa decode", dtype, m, k, r)
+    x = _x(m, k, 51, cuda, dtype)
+    g = torch.Generator().manual_seed(52)
+    a = [((torch.rand(r, k, generator=g) * 2 - 1) / k ** 0.5).to(dtype).to(cuda) for _ in range(2)]
+    t = [torch.empty(m, r, dtype=dtype, device=cuda) for _ in range(2)]
+    kernels.lora_xa_multi([kernels.lora_job(x, a[i], t[i], 1.5) for i in range(2)], m, r, dtype, x)
+    for i in range(2):
+        ref = 1.5 * (x.float().cpu() @ a[i].float().cpu().t())
+        assert_rel(t[i], ref, what=f"xa {i}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_lora_multi_matches_single(cuda, dtype):
     """The multi-job LoRA launches give the single-job results bit for bit (same kernels, same
     order of arithmetic), with jobs on column ranges of a stacked gradient."""
@@ -285,3 +305,76 @@ def test_swiglu_epilogue(cuda, m, inter, k, dtype):
     d = dh.float().cpu()
     assert_rel(dgu[:, :inter], d * u * sig * (1.0 + g * (1.0 - sig)), what="dG")
     assert_rel(dgu[:, inter:], d * g * sig, what="dU")
+
+
+def _scaled_codes(p, qs, dtype):
+    from tests.gpu_util import to_oracle_state
+
+    pn, st = to_oracle_state(p, qs)
+    w = o.dequantize_scaled_codes(pn, st, "bf16" if dtype == torch.bfloat16 else "f16")
+    return torch.from_numpy(w.view(np.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("shapes,bs,nested", [([(384, 256)], 64, True), ([(200, 512)], 128, True),
+                                              ([(136, 320)], 64, False),
+                                              ([(256, 512), (64, 512), (64, 512)], 64, True)])
+def test_rows_decode_one_hot_is_exact(cuda, m, shapes, bs, nested, dtype):
+    """The row-streaming decode path (M <= 2): token t one-hot at column c_t returns the weight
+    column c_t as the GEMV multiplies it - round(fp32(round(code)) * absmax) - bit for bit, over
+    every row of every stacked segment, for columns spread over the reduction."""
+    from solution import kernels
+
+    banner("rows decode one-hot", m, shapes, bs, nested, dtype)
+    ws = [random_weight(n, k, seed=7 * n + k + i, dev=cuda, blocksize=bs, nested=nested)
+          for i, (n, k) in enumerate(shapes)]
+    k = shapes[0][1]
+    ref = torch.cat([_scaled_codes(p, q, dtype) for p, q in ws])  # [sum rows, K] bits
+    for c0 in range(0, k, max(1, k // 6)):
+        cols = [(c0 + 37 * t) % k for t in range(m)]
+        x = torch.zeros(m, k, dtype=dtype)
+        x[torch.arange(m), cols] = 1.0
+        y = kernels.linear_fwd(x.to(cuda), ws)
+        assert torch.equal(y.cpu().view(torch.int16), ref[:, cols].t()), (c0, cols)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_rows_decode_qkv_bias_lora(cuda, m, dtype):
+    """Stacked q|k|v with bias and LoRA on q and v at M <= 4 tokens (the row-streaming path up to
+    2 tokens, the decode kernel above) against fp32 on the oracle's weight (the row-streaming
+    path's rounding of the code table is inside the tolerance)."""
+    from solution import kernels
+
+    banner("rows decode q|k|v + bias + LoRA", m, dtype)
+    k, r, s = 1536, 16, 2.0
+    segs = [random_weight(n, k, seed=300 + i, dev=cuda) for i, n in enumerate((1536, 256, 256))]
+    wname = "bf16" if dtype == torch.bfloat16 else "f16"
+    w = torch.cat([oracle_w16(p, q, wname) for p, q in segs])
+    x = _x(m, k, 11, cuda, dtype)
+    bias = _x(1, 2048, 12, cuda, dtype, std=0.5).view(-1)
+    g = torch.Generator().manual_seed(13)
+    a_q = ((torch.rand(r, k, generator=g) * 2 - 1) / np.sqrt(k)).to(dtype).to(cuda)
+    a_v = ((torch.rand(r, k, generator=g) * 2 - 1) / np.sqrt(k)).to(dtype).to(cuda)
+    b_q = (torch.randn(1536, r, generator=g) * 0.05).to(dtype).to(cuda)
+    b_v = (torch.randn(256, r, generator=g) * 0.05).to(dtype).to(cuda)
+    t_q, t_v = kernels.lora_xa(x, a_q), kernels.lora_xa(x, a_v)
+    loras = [kernels.make_lora(0, r, s, t=t_q, b=b_q), kernels.make_lora(2, r, s, t=t_v, b=b_v)]
+    y = kernels.linear_fwd(x, segs, bias, loras)
+    ref = o.linear_fwd(x, w, bias, [(0, 1536, x, a_q, b_q, s), (1792, 256, x, a_v, b_v, s)])
+    assert_rel(y, ref, what=f"q|k|v M={m}")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 512, 18944), (2, 384, 8960), (1, 100, 64), (2, 72, 1024)])
+def test_rows_decode_long_and_odd_rows(cuda, m, n, k):
+    """Long rows (the 7B down projection's K = 18944: 37 units per lane), rows whose K / 8 units
+    leave lanes idle (K = 64, 1024), an output width not a multiple of 8."""
+    from solution import kernels
+
+    banner("rows decode shapes", m, n, k)
+    p, qs = random_weight(n, k, seed=n + k, dev=cuda)
+    x = _x(m, k, 14, cuda)
+    bias = _x(1, n, 15, cuda, std=0.1).view(-1)
+    y = kernels.linear_fwd(x, [(p, qs)], bias)
+    assert_rel(y, o.linear_fwd(x, oracle_w16(p, qs), bias), what=f"M={m} {n}x{k}")

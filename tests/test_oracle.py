@@ -92,6 +92,34 @@ def test_dequant_conversions_match_torch():
     assert torch.equal(bf, t.bfloat16())
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("nested", [True, False])
+def test_scaled_codes_match_torch_and_element_loop(dtype, nested):
+    """The decode GEMV's weight value round(fp32(round(code[nib])) * absmax) restated three ways:
+    the vectorised oracle, torch's own conversions, and an element loop; where the code is
+    exact in the dtype (+-1, 0) it equals the dequantized weight."""
+    _, packed, st = _small((16, 256), nested=nested)
+    got = o.dequantize_scaled_codes(packed, st, dtype).reshape(-1)
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    code = torch.from_numpy(st.code.astype(np.float32)).to(tdt).float()
+    nib = torch.from_numpy(o.nibbles(packed, 16 * 256).astype(np.int64))
+    a = torch.from_numpy(o.absmax_fp32(st))[torch.arange(16 * 256) // st.blocksize]
+    ref = (code[nib] * a).to(tdt)
+    got_t = torch.from_numpy(got.view(np.int16)).view(tdt) if dtype == "bf16" else \
+        torch.from_numpy(got)
+    assert torch.equal(got_t, ref)
+    p = packed.reshape(-1)
+    ab = o.absmax_fp32(st)
+    for i in range(0, 16 * 256, 97):
+        nb = (int(p[i // 2]) >> 4) if i % 2 == 0 else (int(p[i // 2]) & 0xF)
+        c = np.float32(torch.tensor(float(st.code[nb])).to(tdt).float().item())
+        v = np.float32(c * ab[i // st.blocksize])
+        assert torch.equal(torch.tensor(v).to(tdt), ref[i:i + 1].reshape(()))
+    exact = np.isin(nib.numpy(), [0, 7, 15])
+    plain = o.dequantize(packed, st, dtype).reshape(-1)
+    np.testing.assert_array_equal(got[exact].view(np.int16), plain[exact].view(np.int16))
+
+
 def test_bf16_rounding_ties_to_even():
     vals = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8), 1.0 + 2 ** -9,
                      3.0e38, 1e-40], np.float32)
