@@ -1262,28 +1262,34 @@ constexpr int kRowsMaxRows = 64;    // rows per wave: one result lane each
 constexpr int kRowsMaxWaves = 16;
 constexpr int kRowsRing = 2;        // rows of loads in flight per wave
 
-// The map `a.map[0]`: tile_start[s] = first row group of segment s (cumulative), m_tiles = rows
-// per group; a workgroup runs a.rows_groups groups x a.rows_parts K parts, wave w taking part
-// w % rows_parts of group w / rows_parts.
+// The map `a.map[0]`: tile_start[s] = first row group of segment s (cumulative, each segment's
+// groups padded to a multiple of a.rows_groups), m_tiles = rows per group; a workgroup runs
+// a.rows_groups groups x a.rows_parts K parts, wave w taking part w % rows_parts of group
+// w / rows_parts.
 // (4 waves per SIMD are enough: squeezed for more, the compiler reuses registers that loads
 // in flight still target, which waits for them.)
 template <int DT, int MT, int SP>
 __global__ __launch_bounds__(kRowsMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void gemv_rows_kernel(const GemmArgs a) {
     constexpr int RD = kRowsRing;
-    __shared__ uint32_t s_pair[kMaxSeg][256];
-    __shared__ float s_code2[kMaxSeg][256];
+    __shared__ uint32_t s_pair[256];
+    __shared__ float s_code2[256];
     __shared__ float s_part[kRowsMaxWaves][MT][64];
     const int np = a.rows_parts;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int part = wave % np;
-    const int64_t grp = static_cast<int64_t>(blockIdx.x) * a.rows_groups + wave / np;
+    // The workgroup's groups lie in one segment (each segment's groups are padded to whole
+    // workgroups), so its table sits at a fixed LDS address and a lookup's address is the
+    // packed byte times 4 (one shift with a byte select).
     const TileMap &tm = a.map[0];
-    const bool active = grp < tm.tile_start[a.nseg];
-    const int seg = active ? seg_of_tile(a, tm, grp) : 0;
+    const int64_t grp0 = static_cast<int64_t>(blockIdx.x) * a.rows_groups;
+    const int seg = seg_of_tile(a, tm, grp0);
+    const int64_t grp = grp0 + wave / np;
     const DevWeight w = a.w[seg];
-    const int64_t row0 = uniform64(active ? (grp - tm.tile_start[seg]) * tm.m_tiles : 0);
-    const int nrows = active ? static_cast<int>(tm.m_tiles < w.rows - row0 ? tm.m_tiles : w.rows - row0) : 0;
+    const int64_t row0 = uniform64((grp - tm.tile_start[seg]) * tm.m_tiles);
+    const int64_t left = w.rows - row0;  // <= 0 in a segment's padding groups
+    const int nrows = left <= 0 ? 0 : static_cast<int>(tm.m_tiles < left ? tm.m_tiles : left);
+    const int64_t lrow0 = nrows > 0 ? row0 : 0;  // the rows a padding group loads: row 0
     const int64_t K = a.K;
     const int khalf = static_cast<int>(K / 2);
     const int lane = threadIdx.x & 63;
@@ -1300,21 +1306,20 @@ void gemv_rows_kernel(const GemmArgs a) {
     const int64_t nblk = (w.rows * w.cols + w.blocksize - 1) >> w.bs_shift;
     const rsrc_t qr = make_rsrc(w.absmax, w.nested ? (nblk + 3) & ~int64_t(3) : 0);
     const int kb = static_cast<int>(K >> w.bs_shift);  // absmax blocks per row
-    const int qbase = static_cast<int>(row0) * kb;
+    const int qbase = static_cast<int>(lrow0) * kb;
 
-    // The tables: thread i < 256 (every workgroup has at least 512 threads) writes entry i of
-    // each segment's tables after the barrier below.  Their loads go first, from every thread
+    // The tables of the workgroup's segment: thread i < 256 (every workgroup has at least 512
+    // threads) writes entry i before the barrier below.  Their loads go first, from every thread
     // (a branch here would leave them in flight behind the ring loads on some paths, which
     // makes the loop's wait counts conservative).
     const int i = threadIdx.x & 255;
-    uint32_t hi[kMaxSeg], lo2[kMaxSeg], c2[kMaxSeg];
-#pragma unroll
-    for (int s = 0; s < kMaxSeg; ++s) {
-        const rsrc_t cr = make_rsrc(a.w[s].code, s < a.nseg ? 64 : 0);
-        const rsrc_t c2r = make_rsrc(a.w[s].code2, s < a.nseg && a.w[s].nested ? 1024 : 0);
-        hi[s] = bload4(cr, (i >> 4) * 4);
-        lo2[s] = bload4(cr, (i & 15) * 4);
-        c2[s] = bload4(c2r, i * 4);
+    uint32_t hi, lo2, c2;
+    {
+        const rsrc_t cr = make_rsrc(w.code, 64);
+        const rsrc_t c2r = make_rsrc(w.code2, w.nested ? 1024 : 0);
+        hi = bload4(cr, (i >> 4) * 4);
+        lo2 = bload4(cr, (i & 15) * 4);
+        c2 = bload4(c2r, i * 4);
     }
     // LoRA T[m][lane] (dword loads, like the B rows below: no wait here)
     const rsrc_t tr = make_rsrc(lo.t, lora ? (a.M * lo.rank * 2 + 3) & ~int64_t(3) : 0);
@@ -1343,10 +1348,10 @@ void gemv_rows_kernel(const GemmArgs a) {
     int lblk[SP];      // absmax block of this lane's bytes in a slot, relative to the row
 #pragma unroll
     for (int sl = 0; sl < SP; ++sl) lblk[sl] = (2 * (1024 * (slot0 + sl) + 16 * lane)) >> w.bs_shift;
-    const int last = nrows > 0 ? nrows - 1 : 0;  // an inactive wave re-reads row 0 of segment 0
+    const int last = nrows > 0 ? nrows - 1 : 0;
     auto load = [&](int j, int r) {
         const int rr = r < nrows ? r : last;
-        const int64_t row = row0 + rr;
+        const int64_t row = lrow0 + rr;
 #pragma unroll
         for (int sl = 0; sl < SP; ++sl) {
             const int byte = 1024 * (slot0 + sl) + 16 * lane;
@@ -1358,7 +1363,7 @@ void gemv_rows_kernel(const GemmArgs a) {
         lbw[j] = bload4(br, (static_cast<int>(row) * lo.rank + lane) * 2 & ~3);
     };
     // The first rows' loads go out before the table work, so their latency overlaps it; issued
-    // by every wave (an inactive one reads row 0), so that the wait below retires the
+    // by every wave (a padding group's reads row 0), so that the wait below retires the
     // activation loads on every path.
     // Row by row, in the loop's order (interleaved, the loop's wait counts inherit the worst
     // position a row's loads had here).
@@ -1369,13 +1374,9 @@ void gemv_rows_kernel(const GemmArgs a) {
     }
 
     if (threadIdx.x < 256) {  // write the tables (loaded at the top)
-#pragma unroll
-        for (int s = 0; s < kMaxSeg; ++s) {
-            if (s >= a.nseg) break;
-            s_pair[s][i] = static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, hi[s]))) |
-                           (static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, lo2[s]))) << 16);
-            s_code2[s][i] = a.w[s].nested ? __builtin_bit_cast(float, c2[s]) : (i == 0 ? 1.0f : 0.0f);
-        }
+        s_pair[i] = static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, hi))) |
+                    (static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, lo2))) << 16);
+        s_code2[i] = w.nested ? __builtin_bit_cast(float, c2) : (i == 0 ? 1.0f : 0.0f);
     }
     __syncthreads();
 
@@ -1394,8 +1395,8 @@ void gemv_rows_kernel(const GemmArgs a) {
     float res[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) res[m] = 0.0f;
-    const uint32_t *pair = s_pair[seg];
-    const float *code2 = s_code2[seg];
+    const uint32_t *pair = s_pair;
+    const float *code2 = s_code2;
     // Whole rounds of RD rows; the ring slot of a row past the range (a re-read of the last
     // row) is refilled but not computed.
     for (int r0 = 0; r0 < nrows; r0 += RD) {
@@ -1436,7 +1437,7 @@ void gemv_rows_kernel(const GemmArgs a) {
                 }
             }
             {  // LoRA (branch-free: tv is zero without it, and lbw reads zero)
-                const int e = static_cast<int>(row0 + rr) * lo.rank + lane;
+                const int e = static_cast<int>(lrow0 + rr) * lo.rank + lane;
                 const float bv = to_f32<DT>(static_cast<uint16_t>(lbw[j] >> ((e & 1) * 16)));
 #pragma unroll
                 for (int m = 0; m < MT; ++m) acc[m] += lscale * (tv[m] * bv);
@@ -1906,8 +1907,9 @@ Plan plan_rows(int64_t m, const nf4_weight *ws, int nw) {
     int64_t rpw = (rows + slots - 1) / slots;
     if (rpw < 1) rpw = 1;
     if (rpw > kRowsMaxRows) rpw = kRowsMaxRows;
-    int64_t groups = 0;
-    for (int i = 0; i < nw; ++i) groups += (ws[i].rows + rpw - 1) / rpw;
+    int64_t groups = 0;  // padded to whole workgroups per segment
+    for (int i = 0; i < nw; ++i)
+        groups += ((ws[i].rows + rpw - 1) / rpw + groups_per_wg - 1) / groups_per_wg * groups_per_wg;
     Plan p{6, sp, mt, np, groups, static_cast<int>(rpw), 0, 0};
     p.rows_g = groups_per_wg;
     return p;
@@ -2148,8 +2150,10 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
         g.map[0].m_tiles = p.waves;
         g.map[0].tile_start[0] = 0;
         for (int i = 0; i < nw; ++i)
-            g.map[0].tile_start[i + 1] = g.map[0].tile_start[i] + (ws[i].rows + p.waves - 1) / p.waves;
-        const dim3 grid(static_cast<unsigned>((p.tiles + p.rows_g - 1) / p.rows_g));
+            g.map[0].tile_start[i + 1] =
+                g.map[0].tile_start[i] +
+                ((ws[i].rows + p.waves - 1) / p.waves + p.rows_g - 1) / p.rows_g * p.rows_g;
+        const dim3 grid(static_cast<unsigned>(p.tiles / p.rows_g));
         const dim3 block(p.rows_g * p.splits * 64);
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (dtype == NF4_BF16) {
