@@ -270,8 +270,8 @@ def int8_leg(dev, reps=20):
 # ------------------------------------------------- the projection's neighbours (norm, RoPE)
 
 def norm_rope_leg(dtype, dev, reps=20):
-    """RMSNorm (+ residual, + LoRA dropout inputs) and RoPE forward and backward at M=2048 on
-    the Qwen2.5-1.5B shapes (hidden 1536, 12 query heads, 2 key/value heads of 128): GB/s of
+    """RMSNorm (fp32 residual stream + o_proj output, LoRA dropout inputs with bit-packed masks)
+    and RoPE forward and backward at M=2048 on the Qwen2.5-1.5B shapes (hidden 1536, 12 query heads, 2 key/value heads of 128): GB/s of
     algorithmic bytes against the 8 TB/s HBM peak, each kernel replayed 20 times in a HIP
     graph (these launches are a few microseconds each)."""
     import torch
@@ -281,23 +281,29 @@ def norm_rope_leg(dtype, dev, reps=20):
     h, nh, nkv, hd = 1536, 12, 2, 128
     g = torch.Generator(device=dev).manual_seed(301)
     r = lambda *s: torch.randn(*s, generator=g, device=dev).to(dtype)  # noqa: E731
-    x, d, dy, dq, dv, dres = (r(M, h) for _ in range(6))
+    d, dy, dq, dv = (r(M, h) for _ in range(4))
+    # the residual stream and its gradient in fp32, as the reference's decoder layer keeps them
+    x, dres = (torch.randn(M, h, generator=g, device=dev) for _ in range(2))
     w = torch.rand(h, generator=g, device=dev) + 0.5
-    keep = lambda: (torch.rand(M, h, generator=g, device=dev) > 0.1).to(torch.uint8)  # noqa: E731
+    keep = lambda: torch.rand(M, h, generator=g, device=dev) > 0.1  # noqa: E731
     kq, kv = keep(), keep()
-    _, rstd = kernels.add_rmsnorm(x, w, 1e-6, d=d)
+    _, rstd, _, _, packed = kernels.add_rmsnorm(x, w, 1e-6, d=d, keep_q=kq, keep_v=kv)
     qkv = r(M, (nh + 2 * nkv) * hd)
     ang = torch.rand(M, hd // 2, generator=g, device=dev)
     cos, sin = torch.cat([ang.cos()] * 2, 1), torch.cat([ang.sin()] * 2, 1)
     gq, gk, gv = (r(M, nh, hd) for _ in range(3))
     e = 2  # bytes per element
     legs = {
+        # mode 1: one-byte keep masks in, packed bits out; mode 2: packed bits in
         "rmsnorm_fwd": (lambda: kernels.add_rmsnorm(x, w, 1e-6, d=d, keep_q=kq, keep_v=kv,
                                                     scale_q=1.1, scale_v=1.1),
-                        M * h * (2 * e + 2 + 3 * e) + M * 4 + h * 4),
+                        M * h * (4 + e + 2 + 3 * e) + M * h // 4 + M * 4 + h * 4),
+        "rmsnorm_fwd_packed": (lambda: kernels.add_rmsnorm(x, w, 1e-6, d=d, packed=packed,
+                                                           scale_q=1.1, scale_v=1.1),
+                               M * h * (4 + e + 3 * e) + M * h // 4 + M * 4 + h * 4),
         "rmsnorm_bwd": (lambda: kernels.rmsnorm_bwd(x, w, rstd, dy=dy, d=d, dres=dres, dq=dq, dv=dv,
-                                                    keep_q=kq, keep_v=kv),
-                        M * h * (6 * e + 2 + e) + M * 4 + h * 4),
+                                                    packed=packed),
+                        M * h * (4 * e + 4 + 4 + 4) + M * h // 4 + M * 4 + h * 4),
         "rope_fwd": (lambda: kernels.qkv_rope(qkv, cos, sin, nh, nkv, hd),
                      M * ((nh + 2 * nkv) * hd * e + 2 * hd * 4 + 3 * nh * hd * e + 2 * nkv * hd * e)),
         "rope_bwd": (lambda: kernels.qkv_rope_bwd(gq, gk, gv, cos, sin, nkv),

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NF4_ABI_VERSION 1
+#define NF4_ABI_VERSION 2
 
 /* status codes */
 #define NF4_OK 0
@@ -224,6 +224,14 @@ typedef struct nf4_lora_job {
 /* t_j = in_j @ A_j^T for every job (nf4_lora_xa per job: layer.py:875, 877). */
 int nf4_lora_xa_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
                       void *stream);
+/* out_j = scale_j * in_j @ A_j for every job, the LoRA term of the input gradient on its own:
+ * in_j = da [M, rank] (row stride ld >= rank), w_j = A [rank, cols], out_j [M, cols]
+ * contiguous in the GEMM dtype, fp32 sums rounded once.  For a LoRA input that is not the
+ * projection's input x (dropout p > 0), whose gradient the norm backward masks
+ * (nf4_rmsnorm_bwd's dq / dv).
+ * Replaces: dd_q = da_q @ A_q, dd_v = da_v @ A_v (/root/reference/solution/layer.py:1086-1087). */
+int nf4_lora_ax_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
+                      void *stream);
 /* da_j = scale_j * in_j @ B_j for every job (nf4_lora_da per job: layer.py:1074-1078). */
 int nf4_lora_da_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
                       void *stream);
@@ -312,23 +320,31 @@ int nf4_int8_swiglu_bwd(const int32_t *acc, int64_t m, int64_t inter, int64_t ld
 
 /* One row per token (contiguous [rows, cols] tensors, cols a multiple of 8, at most 8192):
  * h = x (+ d), rstd[r] = 1 / sqrt(mean(h^2) + eps), y = w * (h * rstd) in fp32 rounded once to
- * dtype; w is fp32 [cols].  With keep masks (uint8 [rows, cols], 1 = kept, both or neither) also
- * LoRA's dropout inputs oq = y * keep_q * scale_q, ov = y * keep_v * scale_v.  d may be NULL.
- * Replaces: add_rmsnorm_fwd_kernel (/root/reference/solution/layer.py:92-132; its masks are
- *           packed 8 per byte, here one byte per element). */
-int nf4_add_rmsnorm(const void *x, const void *d, const float *w, void *y, float *rstd,
-                    const uint8_t *keep_q, const uint8_t *keep_v, float scale_q, float scale_v,
-                    void *oq, void *ov, int64_t rows, int64_t cols, float eps, int dtype,
-                    void *stream);
+ * dtype; w is fp32 [cols].  x is the residual stream in res_dtype (NF4_F32, or dtype); d (the
+ * o_proj output, may be NULL), y, oq and ov are in dtype.
+ * LoRA dropout (drop_mode 1 or 2) also writes the dropout inputs oq = y * keep_q * scale_q and
+ * ov = y * keep_v * scale_v (scale = 1 / (1 - p)), each rounded once.  The keep masks live
+ * packed: packed[r][0][j] bit k = keep_q of element 8 j + k, packed[r][1][j] the same for v
+ * ([rows][2][cols / 8] bytes).  Mode 1 reads one-byte 0/1 masks keep_q, keep_v [*, cols]
+ * (8-byte aligned) at row src_rows[r] (row r when src_rows is NULL: the token's row of masks
+ * drawn over a padded batch) and writes their bits to packed; mode 2 reads packed.
+ * Replaces: add_rmsnorm_fwd_kernel with _pack_bits / _unpack_bits
+ *           (/root/reference/solution/layer.py:76-132). */
+int nf4_add_rmsnorm(const void *x, int res_dtype, const void *d, const float *w, void *y,
+                    float *rstd, const uint8_t *keep_q, const uint8_t *keep_v,
+                    const int64_t *src_rows, uint8_t *packed, int drop_mode, float scale_q,
+                    float scale_v, void *oq, void *ov, int64_t rows, int64_t cols, float eps,
+                    int dtype, void *stream);
 
-/* The gradient of the above: g = dy (+ dq * keep_q * scale_q + dv * keep_v * scale_v),
- * h = x (+ d) recomputed, h^ = h * rstd, dx = rstd * (g w - h^ * mean(g w h^)) (+ dres).
- * dy, dq/dv (together with the masks), d and dres may be NULL.
+/* The gradient of the above: g = dy (+ dq * keep_q * scale_q + dv * keep_v * scale_v, the
+ * keep bits read from packed), h = x (+ d) recomputed, h^ = h * rstd,
+ * dx = rstd * (g w - h^ * mean(g w h^)) (+ dres).  dy, dq, dv and d in dtype; x, dres and dx in
+ * res_dtype.  dy, dq/dv (together, with packed), d and dres may be NULL.
  * Replaces: rmsnorm_bwd_lora_kernel (/root/reference/solution/layer.py:135-164). */
-int nf4_rmsnorm_bwd(const void *dy, const void *dq, const void *dv, const uint8_t *keep_q,
-                    const uint8_t *keep_v, float scale_q, float scale_v, const void *x,
-                    const void *d, const float *w, const float *rstd, const void *dres, void *dx,
-                    int64_t rows, int64_t cols, int dtype, void *stream);
+int nf4_rmsnorm_bwd(const void *dy, const void *dq, const void *dv, const uint8_t *packed,
+                    float scale_q, float scale_v, const void *x, int res_dtype, const void *d,
+                    const float *w, const float *rstd, const void *dres, void *dx, int64_t rows,
+                    int64_t cols, int dtype, void *stream);
 
 /* Rotary embedding of the finished q|k|v projection (qkv [tokens, ld_qkv], columns n_heads q
  * heads, n_kv k heads, n_kv v heads of head_dim each; the LoRA terms are already in it, added by

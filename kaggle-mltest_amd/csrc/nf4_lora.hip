@@ -176,6 +176,40 @@ __global__ __launch_bounds__(256) void rowvec_kernel(const Jobs jobs, int64_t m)
     }
 }
 
+// The LoRA term of the input gradient, unfolded (the dropout-masked branch of the norm
+// backward needs it on its own): out[m][k] = scale * sum_j da[m][j] A[j][k] for a job with
+// in = da [M, rank] (row stride ld), w = A [rank, cols], out [M, cols] contiguous.  A thread
+// owns one column k (A's column in registers) over a block of kAxRows rows whose da rows are
+// staged in LDS; fp32 sums over j in order, rounded once.  Bound by the output's writes.
+constexpr int kAxRows = 16;
+
+template <int DT>
+__global__ __launch_bounds__(256) void lora_ax_kernel(const Jobs jobs, int64_t m, int rank) {
+    __shared__ float s_da[kAxRows][kMaxRank];
+    const Job &jb = jobs.j[blockIdx.z];
+    const int64_t k = jb.cols;
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kAxRows;
+    for (int i = threadIdx.x; i < kAxRows * rank; i += 256) {
+        const int r = i / rank, j = i - r * rank;
+        s_da[r][j] = m0 + r < m ? ld1<DT>(jb.in + (m0 + r) * jb.ld + j) : 0.0f;
+    }
+    float a[kMaxRank];
+#pragma unroll
+    for (int j = 0; j < kMaxRank; ++j) a[j] = (j < rank && col < k) ? ld1<DT>(jb.w + j * k + col) : 0.0f;
+    __syncthreads();
+    if (col >= k) return;
+    uint16_t *out = static_cast<uint16_t *>(jb.out);
+    for (int r = 0; r < kAxRows; ++r) {
+        if (m0 + r >= m) break;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMaxRank; ++j)
+            if (j < rank) acc += s_da[r][j] * a[j];
+        out[(m0 + r) * k + col] = st1<DT>(acc * jb.scale);
+    }
+}
+
 // Partial sums over a chunk of rows on v_mfma_f32_16x16x32:
 //   part[chunk][p][j] = sum_{m in chunk} U[m][p] * V[m][j]
 // for a 64-column tile of p (4 waves x 16) and one 16-wide tile of j (blockIdx.z).  Both
@@ -476,6 +510,32 @@ extern "C" int nf4_lora_xa_multi(const nf4_lora_job *jobs, int njobs, int64_t m,
 extern "C" int nf4_lora_da_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank,
                                  int dtype, void *stream) {
     return rowdot_multi<true>(jobs, njobs, m, rank, dtype, stream);
+}
+
+extern "C" int nf4_lora_ax_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank,
+                                 int dtype, void *stream) {
+    if ((dtype != NF4_F16 && dtype != NF4_BF16) || m < 0 || rank < 1 || rank > kMaxRank)
+        return NF4_ERR_ARG;
+    if (!jobs || njobs < 1 || njobs > NF4_MAX_LORA_JOBS) return NF4_ERR_ARG;
+    int64_t maxk = 0;
+    for (int i = 0; i < njobs; ++i) {
+        const nf4_lora_job &j = jobs[i];
+        if (j.cols < 0 || j.ld < rank || !j.out) return NF4_ERR_ARG;
+        if (m > 0 && j.cols > 0 && (!j.in || !j.w)) return NF4_ERR_ARG;
+        maxk = j.cols > maxk ? j.cols : maxk;
+    }
+    if (m == 0 || maxk == 0) return NF4_OK;
+    if ((m + kAxRows - 1) / kAxRows > 65535 || (maxk + 255) / 256 > 0x7fffffff)
+        return NF4_ERR_UNSUPPORTED;
+    Jobs J = to_jobs(jobs, njobs);
+    const dim3 grid(static_cast<unsigned>((maxk + 255) / 256),
+                    static_cast<unsigned>((m + kAxRows - 1) / kAxRows), static_cast<unsigned>(njobs));
+    auto s = static_cast<hipStream_t>(stream);
+    if (dtype == NF4_BF16)
+        hipLaunchKernelGGL(lora_ax_kernel<NF4_BF16>, grid, dim3(256), 0, s, J, m, rank);
+    else
+        hipLaunchKernelGGL(lora_ax_kernel<NF4_F16>, grid, dim3(256), 0, s, J, m, rank);
+    return status_of(hipGetLastError());
 }
 
 extern "C" int nf4_lora_xa(const void *xd, int64_t m, int64_t k, int64_t ldx, const void *a,

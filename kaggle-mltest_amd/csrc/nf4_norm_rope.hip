@@ -54,7 +54,47 @@ __device__ __forceinline__ void store8(uint16_t *p, const float (&v)[8]) {
 }
 
 constexpr int kNormThreads = 256;
-constexpr int kNormChunks = 4;  // 16-byte chunks per thread: rows up to 8192 elements
+constexpr int kNormChunks = 4;  // 8-element chunks per thread: rows up to 8192 elements
+
+// 8 consecutive values of the residual stream (fp32, or the GEMM dtype when RT == DT) <-> 8
+// floats.
+template <int DT, int RT>
+__device__ __forceinline__ void load8r(const void *p, int64_t o, float (&v)[8]) {
+    if constexpr (RT == NF4_F32) {
+        const float4_t a = *reinterpret_cast<const float4_t *>(static_cast<const float *>(p) + o);
+        const float4_t b = *reinterpret_cast<const float4_t *>(static_cast<const float *>(p) + o + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = a[i];
+            v[4 + i] = b[i];
+        }
+    } else {
+        load8<DT>(static_cast<const uint16_t *>(p) + o, v);
+    }
+}
+
+template <int DT, int RT>
+__device__ __forceinline__ void store8r(void *p, int64_t o, const float (&v)[8]) {
+    if constexpr (RT == NF4_F32) {
+        float *q = static_cast<float *>(p) + o;
+        *reinterpret_cast<float4_t *>(q) = (float4_t){v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<float4_t *>(q + 4) = (float4_t){v[4], v[5], v[6], v[7]};
+    } else {
+        store8<DT>(static_cast<uint16_t *>(p) + o, v);
+    }
+}
+
+// The packed keep bits of one 8-element chunk: bit i of the byte = element i (layer.py:76-90).
+__device__ __forceinline__ uint32_t pack8(const uint8_t *keep) {
+    const u32x2_t k = *reinterpret_cast<const u32x2_t *>(keep);
+    uint32_t b = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        b |= ((k.x >> (8 * i)) & 1u) << i;
+        b |= ((k.y >> (8 * i)) & 1u) << (4 + i);
+    }
+    return b;
+}
 
 // Sum over the workgroup (4 waves): wave reductions through cross-lane shuffles, then the four
 // wave sums in LDS in wave order, so every thread gets the same value.
@@ -68,15 +108,23 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// One row per workgroup: h = x (+ d) in fp32, rstd = 1 / sqrt(mean(h^2) + eps),
-// y = w * (h * rstd) rounded to DT; with keep masks also LoRA's dropout inputs
-// oq = y * keep_q * scale_q and ov = y * keep_v * scale_v (layer.py:92-132, masks one byte per
-// element instead of the reference's 8 per byte).
-template <int DT>
+struct NormDrop {
+    const uint8_t *keep_q, *keep_v;  // mode 1: one byte per element, rows src_rows[r] (or r)
+    const int64_t *src_rows;
+    uint8_t *packed;                 // [rows][2][cols / 8]: q's bits, then v's
+    int mode;                        // 0 none, 1 pack from keep_q / keep_v, 2 read packed
+    float scale_q, scale_v;
+};
+
+// One row per workgroup (layer.py:92-132): h = x (+ d) in fp32, rstd = 1 / sqrt(mean(h^2)
+// + eps), y = w * (h * rstd) rounded to DT; with dropout also LoRA's two inputs
+// oq = y * keep_q * scale_q and ov = y * keep_v * scale_v, each rounded once.  A thread's
+// 8-element chunk ch is bit byte ch of the row's packed masks.  x is the residual stream in RT
+// (fp32 or DT), d the output of o_proj in DT.
+template <int DT, int RT>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
-    const uint16_t *x, const uint16_t *d, const float *w, uint16_t *y, float *rstd_out,
-    const uint8_t *keep_q, const uint8_t *keep_v, float scale_q, float scale_v, uint16_t *oq,
-    uint16_t *ov, int64_t cols, float eps) {
+    const void *x, const uint16_t *d, const float *w, uint16_t *y, float *rstd_out,
+    const NormDrop drop, uint16_t *oq, uint16_t *ov, int64_t cols, float eps) {
     __shared__ float red[4];
     const int64_t row = blockIdx.x;
     const int64_t base = row * cols;
@@ -87,7 +135,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     for (int c = 0; c < kNormChunks; ++c) {
         const int ch = threadIdx.x + c * kNormThreads;
         if (ch >= chunks) continue;
-        load8<DT>(x + base + ch * 8, h[c]);
+        load8r<DT, RT>(x, base + ch * 8, h[c]);
         if (d) {
             float e[8];
             load8<DT>(d + base + ch * 8, e);
@@ -100,6 +148,8 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     ss = block_sum(ss, red);
     const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
     if (threadIdx.x == 0) rstd_out[row] = rstd;
+    const int64_t src = drop.mode == 1 && drop.src_rows ? drop.src_rows[row] : row;
+    uint8_t *bits = drop.mode != 0 ? drop.packed + row * 2 * chunks : nullptr;
 #pragma unroll
     for (int c = 0; c < kNormChunks; ++c) {
         const int ch = threadIdx.x + c * kNormThreads;
@@ -108,12 +158,22 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = w[ch * 8 + i] * (h[c][i] * rstd);
         store8<DT>(y + base + ch * 8, v);
-        if (keep_q) {
+        if (drop.mode != 0) {
+            uint32_t bq, bv;
+            if (drop.mode == 1) {
+                bq = pack8(drop.keep_q + src * cols + ch * 8);
+                bv = pack8(drop.keep_v + src * cols + ch * 8);
+                bits[ch] = static_cast<uint8_t>(bq);
+                bits[chunks + ch] = static_cast<uint8_t>(bv);
+            } else {
+                bq = bits[ch];
+                bv = bits[chunks + ch];
+            }
             float q[8], vv[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                q[i] = v[i] * static_cast<float>(keep_q[base + ch * 8 + i]) * scale_q;
-                vv[i] = v[i] * static_cast<float>(keep_v[base + ch * 8 + i]) * scale_v;
+                q[i] = v[i] * static_cast<float>((bq >> i) & 1u) * drop.scale_q;
+                vv[i] = v[i] * static_cast<float>((bv >> i) & 1u) * drop.scale_v;
             }
             store8<DT>(oq + base + ch * 8, q);
             store8<DT>(ov + base + ch * 8, vv);
@@ -122,18 +182,20 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
 }
 
 // One row per workgroup (layer.py:135-164): g = dy (+ dq * keep_q * scale_q
-// + dv * keep_v * scale_v), h = x (+ d) recomputed, h^ = h * rstd, gw = g * w,
-// dx = rstd * (gw - h^ * mean(gw * h^)) (+ dres).
-template <int DT>
+// + dv * keep_v * scale_v, keep bits from the packed masks), h = x (+ d) recomputed,
+// h^ = h * rstd, gw = g * w, dx = rstd * (gw - h^ * mean(gw * h^)) (+ dres).  x, dres and dx
+// are the residual stream in RT; dy, dq, dv and d in DT.
+template <int DT, int RT>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
-    const uint16_t *dy, const uint16_t *dq, const uint16_t *dv, const uint8_t *keep_q,
-    const uint8_t *keep_v, float scale_q, float scale_v, const uint16_t *x, const uint16_t *d,
-    const float *w, const float *rstd_in, const uint16_t *dres, uint16_t *dx, int64_t cols) {
+    const uint16_t *dy, const uint16_t *dq, const uint16_t *dv, const uint8_t *packed,
+    float scale_q, float scale_v, const void *x, const uint16_t *d, const float *w,
+    const float *rstd_in, const void *dres, void *dx, int64_t cols) {
     __shared__ float red[4];
     const int64_t row = blockIdx.x;
     const int64_t base = row * cols;
     const int chunks = static_cast<int>(cols / 8);
     const float rstd = rstd_in[row];
+    const uint8_t *bits = dq ? packed + row * 2 * chunks : nullptr;
     float gw[kNormChunks][8], hh[kNormChunks][8];
     float proj = 0.f;
 #pragma unroll
@@ -147,13 +209,14 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
             float a[8], b[8];
             load8<DT>(dq + o, a);
             load8<DT>(dv + o, b);
+            const uint32_t bq = bits[ch], bv = bits[chunks + ch];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                g[i] += a[i] * static_cast<float>(keep_q[o + i]) * scale_q;
-                g[i] += b[i] * static_cast<float>(keep_v[o + i]) * scale_v;
+                g[i] += a[i] * static_cast<float>((bq >> i) & 1u) * scale_q;
+                g[i] += b[i] * static_cast<float>((bv >> i) & 1u) * scale_v;
             }
         }
-        load8<DT>(x + o, hh[c]);
+        load8r<DT, RT>(x, o, hh[c]);
         if (d) {
             float e[8];
             load8<DT>(d + o, e);
@@ -174,10 +237,10 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_bwd_kernel(
         if (ch >= chunks) continue;
         const int64_t o = base + ch * 8;
         float v[8], r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (dres) load8<DT>(dres + o, r);
+        if (dres) load8r<DT, RT>(dres, o, r);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = rstd * (gw[c][i] - hh[c][i] * proj) + r[i];
-        store8<DT>(dx + o, v);
+        store8r<DT, RT>(dx, o, v);
     }
 }
 
@@ -451,41 +514,53 @@ int rope_shape_ok(int64_t tokens, int n_heads, int n_kv, int head_dim, int dtype
 
 }  // namespace
 
-extern "C" int nf4_add_rmsnorm(const void *x, const void *d, const float *w, void *y, float *rstd,
-                               const uint8_t *keep_q, const uint8_t *keep_v, float scale_q,
-                               float scale_v, void *oq, void *ov, int64_t rows, int64_t cols,
-                               float eps, int dtype, void *stream) {
+extern "C" int nf4_add_rmsnorm(const void *x, int res_dtype, const void *d, const float *w,
+                               void *y, float *rstd, const uint8_t *keep_q,
+                               const uint8_t *keep_v, const int64_t *src_rows, uint8_t *packed,
+                               int drop_mode, float scale_q, float scale_v, void *oq, void *ov,
+                               int64_t rows, int64_t cols, float eps, int dtype, void *stream) {
     int st = norm_shape_ok(rows, cols, dtype);
     if (st != NF4_OK) return st;
+    if (res_dtype != dtype && res_dtype != NF4_F32) return NF4_ERR_ARG;
     if (rows > 0 && (!x || !w || !y || !rstd)) return NF4_ERR_ARG;
-    if ((keep_q != nullptr) != (keep_v != nullptr) || (keep_q && (!oq || !ov))) return NF4_ERR_ARG;
+    if (drop_mode < 0 || drop_mode > 2) return NF4_ERR_ARG;
+    if (drop_mode != 0 && (!packed || !oq || !ov)) return NF4_ERR_ARG;
+    if (drop_mode == 1 && (!keep_q || !keep_v)) return NF4_ERR_ARG;
     for (const void *p : {x, d, static_cast<const void *>(y), static_cast<const void *>(oq),
                           static_cast<const void *>(ov)})
         if (p && !aligned(p, 16)) return NF4_ERR_UNSUPPORTED;
+    if (drop_mode == 1 && (!aligned(keep_q, 8) || !aligned(keep_v, 8))) return NF4_ERR_UNSUPPORTED;
     if (rows == 0) return NF4_OK;
     if (rows > 0x7fffffff) return NF4_ERR_ARG;
     auto s = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(rows));
-    auto X = static_cast<const uint16_t *>(x), D = static_cast<const uint16_t *>(d);
+    const NormDrop dr{keep_q, keep_v, src_rows, packed, drop_mode, scale_q, scale_v};
+    auto D = static_cast<const uint16_t *>(d);
     auto Y = static_cast<uint16_t *>(y), Q = static_cast<uint16_t *>(oq), V = static_cast<uint16_t *>(ov);
-    if (dtype == NF4_BF16)
-        hipLaunchKernelGGL(add_rmsnorm_kernel<NF4_BF16>, grid, dim3(kNormThreads), 0, s, X, D, w, Y,
-                           rstd, keep_q, keep_v, scale_q, scale_v, Q, V, cols, eps);
-    else
-        hipLaunchKernelGGL(add_rmsnorm_kernel<NF4_F16>, grid, dim3(kNormThreads), 0, s, X, D, w, Y,
-                           rstd, keep_q, keep_v, scale_q, scale_v, Q, V, cols, eps);
+#define NF4_NORM_FWD(DT, RT)                                                                       \
+    hipLaunchKernelGGL((add_rmsnorm_kernel<DT, RT>), grid, dim3(kNormThreads), 0, s, x, D, w, Y,  \
+                       rstd, dr, Q, V, cols, eps)
+    if (dtype == NF4_BF16) {
+        if (res_dtype == NF4_F32) NF4_NORM_FWD(NF4_BF16, NF4_F32);
+        else NF4_NORM_FWD(NF4_BF16, NF4_BF16);
+    } else {
+        if (res_dtype == NF4_F32) NF4_NORM_FWD(NF4_F16, NF4_F32);
+        else NF4_NORM_FWD(NF4_F16, NF4_F16);
+    }
+#undef NF4_NORM_FWD
     return status_of(hipGetLastError());
 }
 
 extern "C" int nf4_rmsnorm_bwd(const void *dy, const void *dq, const void *dv,
-                               const uint8_t *keep_q, const uint8_t *keep_v, float scale_q,
-                               float scale_v, const void *x, const void *d, const float *w,
-                               const float *rstd, const void *dres, void *dx, int64_t rows,
-                               int64_t cols, int dtype, void *stream) {
+                               const uint8_t *packed, float scale_q, float scale_v, const void *x,
+                               int res_dtype, const void *d, const float *w, const float *rstd,
+                               const void *dres, void *dx, int64_t rows, int64_t cols, int dtype,
+                               void *stream) {
     int st = norm_shape_ok(rows, cols, dtype);
     if (st != NF4_OK) return st;
+    if (res_dtype != dtype && res_dtype != NF4_F32) return NF4_ERR_ARG;
     if (rows > 0 && (!x || !w || !rstd || !dx)) return NF4_ERR_ARG;
-    if ((dq != nullptr) != (dv != nullptr) || (dq && (!keep_q || !keep_v))) return NF4_ERR_ARG;
+    if ((dq != nullptr) != (dv != nullptr) || (dq && !packed)) return NF4_ERR_ARG;
     for (const void *p : {dy, dq, dv, x, d, dres, static_cast<const void *>(dx)})
         if (p && !aligned(p, 16)) return NF4_ERR_UNSUPPORTED;
     if (rows == 0) return NF4_OK;
@@ -493,14 +568,17 @@ extern "C" int nf4_rmsnorm_bwd(const void *dy, const void *dq, const void *dv,
     auto s = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(rows));
     auto P = [](const void *p) { return static_cast<const uint16_t *>(p); };
-    if (dtype == NF4_BF16)
-        hipLaunchKernelGGL(rmsnorm_bwd_kernel<NF4_BF16>, grid, dim3(kNormThreads), 0, s, P(dy), P(dq),
-                           P(dv), keep_q, keep_v, scale_q, scale_v, P(x), P(d), w, rstd, P(dres),
-                           static_cast<uint16_t *>(dx), cols);
-    else
-        hipLaunchKernelGGL(rmsnorm_bwd_kernel<NF4_F16>, grid, dim3(kNormThreads), 0, s, P(dy), P(dq),
-                           P(dv), keep_q, keep_v, scale_q, scale_v, P(x), P(d), w, rstd, P(dres),
-                           static_cast<uint16_t *>(dx), cols);
+#define NF4_NORM_BWD(DT, RT)                                                                       \
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<DT, RT>), grid, dim3(kNormThreads), 0, s, P(dy), P(dq), \
+                       P(dv), packed, scale_q, scale_v, x, P(d), w, rstd, dres, dx, cols)
+    if (dtype == NF4_BF16) {
+        if (res_dtype == NF4_F32) NF4_NORM_BWD(NF4_BF16, NF4_F32);
+        else NF4_NORM_BWD(NF4_BF16, NF4_BF16);
+    } else {
+        if (res_dtype == NF4_F32) NF4_NORM_BWD(NF4_F16, NF4_F32);
+        else NF4_NORM_BWD(NF4_F16, NF4_F16);
+    }
+#undef NF4_NORM_BWD
     return status_of(hipGetLastError());
 }
 

@@ -312,43 +312,103 @@ def _rows(t, cols):
         raise ValueError("norm operands are contiguous [rows, cols] tensors")
 
 
+def _gemm_dtype(x, *others, dtype=None):
+    """The GEMM dtype of a norm call: `dtype`, else the first 16-bit operand's, else x's."""
+    if dtype is None:
+        for t in (*others, x):
+            if t is not None and t.dtype in (torch.float16, torch.bfloat16):
+                dtype = t.dtype
+                break
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("the norm kernels compute float16 or bfloat16 outputs")
+    if x.dtype not in (dtype, torch.float32):
+        raise ValueError("the residual stream x is float32 or the GEMM dtype")
+    return dtype
+
+
+def _as_u8(keep):
+    keep = keep.contiguous()
+    return keep.view(torch.uint8) if keep.dtype == torch.bool else keep.to(torch.uint8)
+
+
 def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, d: torch.Tensor | None = None,
-                keep_q: torch.Tensor | None = None, keep_v: torch.Tensor | None = None,
+                dtype=None, keep_q: torch.Tensor | None = None, keep_v: torch.Tensor | None = None,
+                rows: torch.Tensor | None = None, packed: torch.Tensor | None = None,
                 scale_q: float = 1.0, scale_v: float = 1.0):
-    """(y, rstd[, oq, ov]): RMSNorm of x (+ d) with fp32 weight w, y in x's dtype; with uint8
-    keep masks also LoRA's dropout inputs y * keep * scale."""
-    _check_device(x, d, w, keep_q, keep_v)
-    rows, cols = x.shape
-    for t in (d, keep_q, keep_v):
-        _rows(t, cols)
+    """RMSNorm of the residual stream x (+ d) (layer.py:92-132, 683-715): returns (y, rstd), y in
+    the GEMM dtype (`dtype`, default d's or x's) and rstd fp32 [rows].  x is fp32 or the GEMM
+    dtype, d the GEMM dtype.  With LoRA dropout also the dropout inputs y * keep * scale:
+      keep_q, keep_v (bool or 0/1 uint8 [*, cols], read at row rows[r], or r when rows is None)
+        -> (y, rstd, oq, ov, packed), packed the masks 8 per byte ([rows, 2 * cols / 8] uint8,
+           q's bytes then v's; bit k of byte j = element 8 j + k);
+      packed -> (y, rstd, oq, ov)."""
+    _check_device(x, d, w, keep_q, keep_v, rows, packed)
+    dtype = _gemm_dtype(x, d, dtype=dtype)
+    n, cols = x.shape
     _rows(x, cols)
-    y = torch.empty_like(x)
-    rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+    _rows(d, cols)
+    y = torch.empty((n, cols), dtype=dtype, device=x.device)
+    rstd = torch.empty(n, dtype=torch.float32, device=x.device)
     w = w.to(torch.float32).contiguous()
-    oq = ov = None
+    mode, oq, ov, kq, kv = 0, None, None, None, None
     if keep_q is not None:
-        oq, ov = torch.empty_like(x), torch.empty_like(x)
-    st = load().nf4_add_rmsnorm(_p(x), _p(d), _p(w), _p(y), _p(rstd), _p(keep_q), _p(keep_v),
-                                float(scale_q), float(scale_v), _p(oq), _p(ov), rows, cols,
-                                float(eps), _code(x.dtype), stream_of(x))
+        if keep_v is None or packed is not None:
+            raise ValueError("give keep_q and keep_v (mode 1) or packed (mode 2)")
+        kq, kv = _as_u8(keep_q), _as_u8(keep_v)
+        if kq.shape[-1] != cols or kv.shape != kq.shape:
+            raise ValueError("keep masks are [*, cols]")
+        if rows is not None:
+            rows = rows.to(torch.int64).contiguous()
+            if rows.numel() != n:
+                raise ValueError("rows holds one mask row per token")
+        elif kq.shape[0] < n:
+            raise ValueError("keep masks need a row per token")
+        packed = torch.empty((n, 2 * (cols // 8)), dtype=torch.uint8, device=x.device)
+        mode = 1
+    elif packed is not None:
+        if tuple(packed.shape) != (n, 2 * (cols // 8)) or packed.dtype != torch.uint8:
+            raise ValueError("packed masks are uint8 [rows, 2 * cols / 8]")
+        packed = packed.contiguous()
+        mode = 2
+    if mode:
+        oq, ov = torch.empty_like(y), torch.empty_like(y)
+    st = load().nf4_add_rmsnorm(_p(x), DTYPE_CODE[x.dtype], _p(d), _p(w), _p(y), _p(rstd), _p(kq),
+                                _p(kv), _p(rows) if mode == 1 else None, _p(packed), mode,
+                                float(scale_q), float(scale_v), _p(oq), _p(ov), n, cols,
+                                float(eps), _code(dtype), stream_of(x))
     check(st, "nf4_add_rmsnorm")
-    return (y, rstd) if keep_q is None else (y, rstd, oq, ov)
+    if mode == 1:
+        return y, rstd, oq, ov, packed
+    if mode == 2:
+        return y, rstd, oq, ov
+    return y, rstd
 
 
 def rmsnorm_bwd(x: torch.Tensor, w: torch.Tensor, rstd: torch.Tensor, dy=None, d=None, dres=None,
-                dq=None, dv=None, keep_q=None, keep_v=None, scale_q: float = 1.0,
-                scale_v: float = 1.0) -> torch.Tensor:
-    """dX of add_rmsnorm from the output's gradient dy and LoRA's dropout branches dq, dv, plus
-    the residual gradient dres."""
-    _check_device(x, w, rstd, dy, d, dres, dq, dv, keep_q, keep_v)
-    rows, cols = x.shape
-    for t in (x, dy, d, dres, dq, dv, keep_q, keep_v):
+                dq=None, dv=None, packed=None, scale_q: float = 1.0, scale_v: float = 1.0,
+                dtype=None) -> torch.Tensor:
+    """dX of add_rmsnorm (layer.py:135-164, 718-730) from the output's gradient dy and LoRA's
+    dropout branches dq, dv (masked with the packed keep bits of the forward), plus the
+    residual gradient dres; dX and dres in x's dtype (fp32 for an fp32 residual stream), the
+    other gradients in the GEMM dtype."""
+    _check_device(x, w, rstd, dy, d, dres, dq, dv, packed)
+    dtype = _gemm_dtype(x, dy, dq, d, dtype=dtype)
+    n, cols = x.shape
+    for t in (x, dy, d, dres, dq, dv):
         _rows(t, cols)
+    if dres is not None and dres.dtype != x.dtype:
+        raise ValueError("dres has the residual stream's dtype")
+    if (dq is None) != (dv is None) or (dq is not None and packed is None):
+        raise ValueError("dq and dv come together, with the packed masks")
+    if packed is not None:
+        if tuple(packed.shape) != (n, 2 * (cols // 8)) or packed.dtype != torch.uint8:
+            raise ValueError("packed masks are uint8 [rows, 2 * cols / 8]")
+        packed = packed.contiguous()
     dx = torch.empty_like(x)
     w = w.to(torch.float32).contiguous()
-    st = load().nf4_rmsnorm_bwd(_p(dy), _p(dq), _p(dv), _p(keep_q), _p(keep_v), float(scale_q),
-                                float(scale_v), _p(x), _p(d), _p(w), _p(rstd), _p(dres), _p(dx),
-                                rows, cols, _code(x.dtype), stream_of(x))
+    st = load().nf4_rmsnorm_bwd(_p(dy), _p(dq), _p(dv), _p(packed), float(scale_q),
+                                float(scale_v), _p(x), DTYPE_CODE[x.dtype], _p(d), _p(w), _p(rstd),
+                                _p(dres), _p(dx), n, cols, _code(dtype), stream_of(x))
     check(st, "nf4_rmsnorm_bwd")
     return dx
 
@@ -426,6 +486,25 @@ def lora_da_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor):
     arr, n = _jobs(jobs)
     check(load().nf4_lora_da_multi(arr, n, m, rank, _code(dtype), stream_of(stream_tensor)),
           "nf4_lora_da_multi")
+
+
+def lora_ax_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor):
+    """out_j = scale_j * da_j @ A_j ([M, K]) for every job (lora_ax_job), one launch."""
+    arr, n = _jobs(jobs)
+    check(load().nf4_lora_ax_multi(arr, n, m, rank, _code(dtype), stream_of(stream_tensor)),
+          "nf4_lora_ax_multi")
+
+
+def lora_ax_job(da: torch.Tensor, a: torch.Tensor, out: torch.Tensor, scale: float = 1.0):
+    """A job of lora_ax_multi: da [M, rank] (any row stride), A [rank, K] contiguous, out
+    [M, K] contiguous."""
+    _check_device(da, a, out)
+    if not a.is_contiguous() or not out.is_contiguous() or da.stride(-1) != 1:
+        raise ValueError("lora_ax: A and out contiguous, da rows contiguous")
+    if out.shape[1] != a.shape[1] or da.shape[1] != a.shape[0] or out.shape[0] != da.shape[0]:
+        raise ValueError("lora_ax: da [M, r], A [r, K], out [M, K]")
+    return NF4LoraJob(in_=da.data_ptr(), ld=da.stride(0), cols=a.shape[1], w=a.data_ptr(),
+                      out=out.data_ptr(), scale=float(scale), transpose_out=0)
 
 
 def lora_wgrad_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor):

@@ -354,6 +354,30 @@ def mlp_fwd(x, wg, wu, wd):
 
 # --------------------------------------------------- the projection's neighbours (fp32)
 
+def pack_keep_bits(keep_q, keep_v) -> np.ndarray:
+    """0/1 keep masks [rows, cols] (cols a multiple of 8) -> uint8 [rows, 2 * cols / 8]: per row
+    q's bytes then v's, bit k of byte j = element 8 j + k (layer.py:76-81, 118-125)."""
+    out = []
+    for keep in (keep_q, keep_v):
+        k = (np.asarray(keep) != 0).astype(np.uint32)
+        rows, cols = k.shape
+        b = (k.reshape(rows, cols // 8, 8) << np.arange(8, dtype=np.uint32)).sum(-1)
+        out.append(b.astype(np.uint8))
+    return np.concatenate(out, axis=1)
+
+
+def unpack_keep_bits(packed, cols):
+    """The inverse of pack_keep_bits: (keep_q, keep_v) as uint8 0/1 [rows, cols]
+    (layer.py:84-90)."""
+    p = np.asarray(packed, dtype=np.uint8)
+    nb = cols // 8
+    res = []
+    for half in (p[:, :nb], p[:, nb:2 * nb]):
+        bits = (half[:, :, None].astype(np.uint32) >> np.arange(8, dtype=np.uint32)) & 1
+        res.append(bits.reshape(p.shape[0], cols).astype(np.uint8))
+    return res[0], res[1]
+
+
 def add_rmsnorm(x, w, eps, d=None, keep_q=None, keep_v=None, scale_q=1.0, scale_v=1.0):
     """fp32 ``h = x (+ d)``, ``rstd = 1/sqrt(mean(h^2) + eps)``, ``y = w * (h * rstd)`` and
     LoRA's dropout inputs ``y * keep * scale`` (layer.py:92-132).  Returns (y, rstd, oq, ov)."""

@@ -244,6 +244,25 @@ def test_lora_xa_decode_sizes(cuda, dtype, m, k, r):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,k,r", [(1, 1536, 16), (37, 3584, 16), (300, 1536, 64), (19, 200, 5)])
+def test_lora_ax(cuda, dtype, m, k, r):
+    """d(xd) = scale * da A ([M, K]) for two jobs of different widths in one launch, against an
+    fp32 product (rounded once, so within the path's tolerance)."""
+    from solution import kernels
+
+    banner("lora ax", dtype, m, k, r)
+    da = [_x(m, r, 61 + i, cuda, dtype) for i in range(2)]
+    g = torch.Generator().manual_seed(63)
+    a = [(torch.randn(r, kk, generator=g) / r ** 0.5).to(dtype).to(cuda) for kk in (k, k // 2 + 8)]
+    out = [torch.empty(m, aa.shape[1], dtype=dtype, device=cuda) for aa in a]
+    kernels.lora_ax_multi([kernels.lora_ax_job(da[i], a[i], out[i], 0.5 + i) for i in range(2)],
+                          m, r, dtype, da[0])
+    for i in range(2):
+        ref = (0.5 + i) * (da[i].float().cpu() @ a[i].float().cpu())
+        assert_rel(out[i], ref, what=f"ax {i}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_lora_multi_matches_single(cuda, dtype):
     """The multi-job LoRA launches give the single-job results bit for bit (same kernels, same
     order of arithmetic), with jobs on column ranges of a stacked gradient."""

@@ -79,6 +79,71 @@ def test_qkv_projection_with_lora_grads(cuda, dtype):
         assert_rel(got, ref.grad, mean_rel=3e-3 if dtype == torch.bfloat16 else 1e-3, what=name)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_qkv_projection_lora_dropout_chain(cuda, dtype):
+    """LoRA dropout p = 0.1 on q and v through the reference's chain (layer.py:859-878,
+    1072-1090, 135-164): RMSNorm of the fp32 residual stream with keep masks drawn over a padded
+    batch (mode 1, packed bits out), the q|k|v projection whose adapters read the dropout
+    outputs, then the backward: the projection's d(drop_q), d(drop_v) masked in the norm
+    backward with the packed bits, plus a residual gradient.  Against fp32 autograd of the same
+    formulas on the CPU with the same masks."""
+    from solution import layer
+    from solution.layer import LoraAdapter, NF4Projection, ProjectionSpec
+
+    banner("LoRA dropout chain p=0.1", dtype)
+    m, k, r, alpha, p = 384, 1536, 16, 32, 0.1
+    s, keep_scale = alpha / r, 1.0 / (1.0 - p)
+    segs = [random_weight(n, k, seed=300 + i, dev=cuda) for i, n in enumerate((1536, 256, 256))]
+    wname = "bf16" if dtype == torch.bfloat16 else "f16"
+    w = torch.cat([oracle_w16(pp, q, wname) for pp, q in segs]).float()
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(m, k, generator=g).to(cuda)                       # fp32 residual stream
+    nw = (torch.rand(k, generator=g) + 0.5).to(cuda)                  # norm weight
+    bias = (torch.randn(2048, generator=g) * 0.5).to(dtype).to(cuda)
+    kq_pad = torch.rand(m + 5, k, generator=g) > p                    # masks over a padded batch
+    kv_pad = torch.rand(m + 5, k, generator=g) > p
+    src = torch.randperm(m + 5, generator=g)[:m]
+    bound = 1 / np.sqrt(k)
+    a_q = ((torch.rand(r, k, generator=g) * 2 - 1) * bound).to(cuda).requires_grad_()
+    a_v = ((torch.rand(r, k, generator=g) * 2 - 1) * bound).to(cuda).requires_grad_()
+    b_q = (torch.randn(1536, r, generator=g) * 0.01).to(cuda).requires_grad_()
+    b_v = (torch.randn(256, r, generator=g) * 0.01).to(cuda).requires_grad_()
+    dy = (torch.randn(m, 2048, generator=g) * 1e-3).to(dtype).to(cuda)
+    dres = (torch.randn(m, k, generator=g) * 1e-3).to(cuda)
+
+    y16, rstd, drop_q, drop_v, packed = layer._norm(
+        x, None, nw, 1e-6, dtype, (kq_pad.to(cuda), kv_pad.to(cuda), src.to(cuda), keep_scale,
+                                   keep_scale))
+    y16, drop_q, drop_v = (t.requires_grad_() for t in (y16, drop_q, drop_v))
+    spec = ProjectionSpec(weights=segs, loras=[LoraAdapter(0, s, own_input=True),
+                                               LoraAdapter(2, s, own_input=True)])
+    y = NF4Projection.apply(y16, bias, spec, a_q, b_q, drop_q, a_v, b_v, drop_v)
+    y.backward(dy)
+    dx = layer._norm_bwd(y16.grad, drop_q.grad, drop_v.grad, packed, x, None, nw, rstd, dres,
+                         keep_scale, keep_scale)
+    assert dx.dtype == torch.float32
+
+    xr = x.cpu().requires_grad_()
+    leaves = [t.detach().float().cpu().requires_grad_() for t in (a_q, b_q, a_v, b_v)]
+    aq, bq, av, bv = leaves
+    kq, kv = kq_pad[src].float(), kv_pad[src].float()
+    rs = 1.0 / (xr.pow(2).mean(-1, keepdim=True) + 1e-6).sqrt()
+    yn = nw.cpu() * (xr * rs)
+    dq_in, dv_in = yn * kq * keep_scale, yn * kv * keep_scale
+    yr = yn @ w.t() + bias.float().cpu()
+    yr = torch.cat([yr[:, :1536] + s * (dq_in @ aq.t()) @ bq.t(), yr[:, 1536:1792],
+                    yr[:, 1792:] + s * (dv_in @ av.t()) @ bv.t()], -1)
+    (yr * dy.float().cpu()).sum().add_((xr * dres.cpu()).sum()).backward()
+    assert_rel(y, yr.detach(), what="y")
+    assert_rel(dx, xr.grad, what="dx")
+    for name, got, ref in zip(("dA_q", "dB_q", "dA_v", "dB_v"), (a_q.grad, b_q.grad, a_v.grad,
+                                                                 b_v.grad), leaves):
+        assert_rel(got, ref.grad, mean_rel=3e-3 if dtype == torch.bfloat16 else 1e-3, what=name)
+    # dropped elements are zero in the dropout inputs
+    assert torch.all(drop_q.detach().cpu()[kq == 0] == 0)
+    assert torch.all(drop_v.detach().cpu()[kv == 0] == 0)
+
+
 @pytest.mark.parametrize("tokens", [200, 8])
 def test_recomputed_mlp_matches_fp32(cuda, tokens):
     """The reference's MLP test shapes (gate/up 1024x512, down 512x1024, x [1, 200, 512]): the

@@ -21,47 +21,75 @@ def _r(shape, seed, dev, dtype, std=1.0):
 
 def _keep(shape, seed, dev):
     g = torch.Generator().manual_seed(seed)
-    return (torch.rand(*shape, generator=g) > 0.1).to(torch.uint8).to(dev)
+    return (torch.rand(*shape, generator=g) > 0.1).to(dev)
+
+
+def _packed(kq, kv):
+    return torch.from_numpy(o.pack_keep_bits(kq.cpu().numpy(), kv.cpu().numpy()))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,cols", [(1, 1536), (37, 3584), (300, 1536), (5, 24)])
+@pytest.mark.parametrize("res32", [False, True])
 @pytest.mark.parametrize("residual,dropout", [(False, False), (True, True)])
-def test_add_rmsnorm(cuda, dtype, rows, cols, residual, dropout):
+def test_add_rmsnorm(cuda, dtype, rows, cols, res32, residual, dropout):
+    """y, rstd and the dropout inputs against the oracle; with dropout, masks drawn over a
+    padded batch of rows + 3 rows and gathered through a token -> row map (mode 1): the packed
+    bits must equal the oracle's packing bit for bit, and feeding them back (mode 2) must give
+    the same outputs bit for bit.  res32: the residual stream x in fp32."""
     from solution import kernels
 
-    banner("rmsnorm fwd", dtype, rows, cols, residual, dropout)
-    x = _r((rows, cols), 1, cuda, dtype)
+    banner("rmsnorm fwd", dtype, rows, cols, res32, residual, dropout)
+    x = _r((rows, cols), 1, cuda, torch.float32 if res32 else dtype)
     d = _r((rows, cols), 2, cuda, dtype, 0.5) if residual else None
     w = (torch.rand(cols, generator=torch.Generator().manual_seed(3)) + 0.5).to(cuda)
-    kq = _keep((rows, cols), 4, cuda) if dropout else None
-    kv = _keep((rows, cols), 5, cuda) if dropout else None
-    out = kernels.add_rmsnorm(x, w, 1e-6, d=d, keep_q=kq, keep_v=kv, scale_q=1.0 / 0.9,
-                              scale_v=1.0 / 0.9)
-    y, rstd = out[0], out[1]
+    if not dropout:
+        y, rstd = kernels.add_rmsnorm(x, w, 1e-6, d=d, dtype=dtype)
+        ry, rr, _, _ = o.add_rmsnorm(x, w, 1e-6, d=d)
+        assert y.dtype == dtype
+        assert_rel(y, ry, what="y")
+        torch.testing.assert_close(rstd.cpu(), rr, rtol=1e-5, atol=0)
+        return
+    kq_pad, kv_pad = _keep((rows + 3, cols), 4, cuda), _keep((rows + 3, cols), 5, cuda)
+    src = torch.randperm(rows + 3, generator=torch.Generator().manual_seed(6))[:rows].to(cuda)
+    y, rstd, oq, ov, packed = kernels.add_rmsnorm(x, w, 1e-6, d=d, dtype=dtype, keep_q=kq_pad,
+                                                  keep_v=kv_pad, rows=src, scale_q=1.0 / 0.9,
+                                                  scale_v=1.0 / 0.8)
+    kq, kv = kq_pad[src], kv_pad[src]
+    assert torch.equal(packed.cpu(), _packed(kq, kv))
     ry, rr, rq, rv = o.add_rmsnorm(x, w, 1e-6, d=d, keep_q=kq, keep_v=kv, scale_q=1.0 / 0.9,
-                                   scale_v=1.0 / 0.9)
+                                   scale_v=1.0 / 0.8)
     assert_rel(y, ry, what="y")
     torch.testing.assert_close(rstd.cpu(), rr, rtol=1e-5, atol=0)
-    if dropout:
-        assert_rel(out[2], rq, what="oq")
-        assert_rel(out[3], rv, what="ov")
+    assert_rel(oq, rq, what="oq")
+    assert_rel(ov, rv, what="ov")
+    y2, rstd2, oq2, ov2 = kernels.add_rmsnorm(x, w, 1e-6, d=d, dtype=dtype, packed=packed,
+                                              scale_q=1.0 / 0.9, scale_v=1.0 / 0.8)
+    for a, b in ((y, y2), (rstd, rstd2), (oq, oq2), (ov, ov2)):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,cols", [(37, 3584), (300, 1536)])
-def test_rmsnorm_bwd(cuda, dtype, rows, cols):
+@pytest.mark.parametrize("res32", [False, True])
+def test_rmsnorm_bwd(cuda, dtype, rows, cols, res32):
+    """dX with every branch (output gradient, LoRA's two masked dropout branches from packed
+    bits, the recomputed residual sum, the residual gradient) against the oracle; res32: x,
+    dres and dX in fp32."""
     from solution import kernels
 
-    banner("rmsnorm bwd", dtype, rows, cols)
-    x, d = _r((rows, cols), 11, cuda, dtype), _r((rows, cols), 12, cuda, dtype, 0.5)
+    banner("rmsnorm bwd", dtype, rows, cols, res32)
+    rt = torch.float32 if res32 else dtype
+    x, d = _r((rows, cols), 11, cuda, rt), _r((rows, cols), 12, cuda, dtype, 0.5)
     w = (torch.rand(cols, generator=torch.Generator().manual_seed(13)) + 0.5).to(cuda)
-    y, rstd = kernels.add_rmsnorm(x, w, 1e-6, d=d)
+    y, rstd = kernels.add_rmsnorm(x, w, 1e-6, d=d, dtype=dtype)
     dy, dq, dv = (_r((rows, cols), s, cuda, dtype, 1e-2) for s in (14, 15, 16))
-    dres = _r((rows, cols), 17, cuda, dtype, 1e-2)
+    dres = _r((rows, cols), 17, cuda, rt, 1e-2)
     kq, kv = _keep((rows, cols), 18, cuda), _keep((rows, cols), 19, cuda)
-    dx = kernels.rmsnorm_bwd(x, w, rstd, dy=dy, d=d, dres=dres, dq=dq, dv=dv, keep_q=kq,
-                             keep_v=kv, scale_q=1.25, scale_v=0.75)
+    packed = _packed(kq, kv).to(cuda)
+    dx = kernels.rmsnorm_bwd(x, w, rstd, dy=dy, d=d, dres=dres, dq=dq, dv=dv, packed=packed,
+                             scale_q=1.25, scale_v=0.75)
+    assert dx.dtype == rt
     ref = o.rmsnorm_bwd(x, w, rstd, dy=dy, d=d, dres=dres, dq=dq, dv=dv, keep_q=kq, keep_v=kv,
                         scale_q=1.25, scale_v=0.75)
     assert_rel(dx, ref, what="dx")

@@ -227,6 +227,31 @@ def _norm_inputs(rows=5, cols=24, seed=0):
     return r(rows, cols), r(rows, cols) * 0.5, r(cols).abs() + 0.5, keep(), keep()
 
 
+def test_keep_bits_known_answer_and_numpy():
+    """The mask packing (layer.py:76-90): bit k of byte j is element 8 j + k, q's bytes before
+    v's in a row.  Pinned by hand-worked bytes and by numpy's little-endian packbits; the
+    unpacking inverts it."""
+    kq = np.zeros((2, 16), np.uint8)
+    kv = np.zeros((2, 16), np.uint8)
+    kq[0, 0] = 1            # element 0 -> byte 0 bit 0
+    kq[0, 9] = 1            # element 9 -> byte 1 bit 1
+    kv[0, 7] = 1            # v element 7 -> v byte 0 bit 7
+    kv[1, 8:16] = 1         # v byte 1 all set
+    p = o.pack_keep_bits(kq, kv)
+    assert p.shape == (2, 4) and p.dtype == np.uint8
+    assert p[0].tolist() == [0x01, 0x02, 0x80, 0x00]
+    assert p[1].tolist() == [0x00, 0x00, 0x00, 0xFF]
+    rng = np.random.default_rng(7)
+    kq = (rng.random((5, 96)) > 0.1).astype(np.uint8)
+    kv = (rng.random((5, 96)) > 0.5).astype(np.uint8)
+    p = o.pack_keep_bits(kq, kv)
+    np.testing.assert_array_equal(p[:, :12], np.packbits(kq, axis=1, bitorder="little"))
+    np.testing.assert_array_equal(p[:, 12:], np.packbits(kv, axis=1, bitorder="little"))
+    uq, uv = o.unpack_keep_bits(p, 96)
+    np.testing.assert_array_equal(uq, kq)
+    np.testing.assert_array_equal(uv, kv)
+
+
 def test_add_rmsnorm_matches_row_loop():
     """The vectorised norm against an explicit per-row, per-element fp64 loop."""
     x, d, w, kq, kv = _norm_inputs()
