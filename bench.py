@@ -430,7 +430,7 @@ def dequant_leg(dtype, dev, reps=5):
         base[name] = (packed.view(-1), qs)
     groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
     grouped, batched, keep = [], [], []
-    total_bytes = 0
+    total_bytes = write_bytes = 0
     for layer in range(28):
         layer_descs, layer_outs = [], []
         for names in groups:
@@ -447,6 +447,7 @@ def dequant_leg(dtype, dev, reps=5):
             arr = (_lib.NF4Weight * len(descs))(*descs)
             grouped.append((arr, len(descs), out.data_ptr()))
             total_bytes += dequant_bytes(rows * cols)
+            write_bytes += 2 * rows * cols
             off = 0
             for d, nm in zip(descs, names):  # the same outputs, weight by weight
                 layer_descs.append(d)
@@ -502,7 +503,8 @@ def dequant_leg(dtype, dev, reps=5):
     copy_ms = _time_steps(torch, lambda: big2.copy_(big), 5, 2)
     del big, big2
     return {"gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4),
-            "bytes_per_pass": total_bytes, "us_per_pass": round(table_ms * 1e3, 1),
+            "bytes_per_pass": total_bytes, "read_bytes": total_bytes - write_bytes,
+            "write_bytes": write_bytes, "us_per_pass": round(table_ms * 1e3, 1),
             "launches_per_pass": 1, "workgroups": int(blocks.value),
             "working_set": "28-layer Qwen2.5-1.5B stack (196 weights)",
             "timing": "one nf4_dequant_table launch over all 196 weights, HIP events, mean of 10",
@@ -599,6 +601,68 @@ def cpu_baseline(dtype_name, reps):
                        f"torch threads {threads}, os.cpu_count() {os.cpu_count()}, CPU {cpu}")}
 
 
+# ------------------------------------------------------------------ measured device ceilings
+
+def measured_peaks(dtype, dev):
+    """What this box sustains, for fractions of measured peaks beside the data-sheet ones: the
+    MFMA rate of back-to-back v_mfma_f32_32x32x16 on register operands (nf4_probe_mfma, 2048
+    workgroups of 4 waves x 4 independent accumulators; operands drawn from N(0, 1), whose bit
+    patterns set the power draw), the HBM read rate (nf4_probe_read over 4 GiB) and write rate
+    (torch fill_ of 4 GiB).  Best of 3 timed launches each."""
+    import torch
+
+    from solution import _lib
+
+    lib = _lib.load()
+    dt = _lib.DTYPE_CODE[dtype]
+    s = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    ops = torch.randn(128 * 8, generator=torch.Generator().manual_seed(7)).to(dtype).to(dev)
+    wgs, iters = 2048, 4000
+    out = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+
+    def best(fn, n=3):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return min(ts)
+
+    def mfma():
+        if lib.nf4_probe_mfma(ops.data_ptr(), wgs, iters, dt, out.data_ptr(), s()):
+            raise RuntimeError("nf4_probe_mfma failed")
+    mfma_ms = best(mfma)
+    flops = 2.0 * 32 * 32 * 16 * 4 * iters * 4 * wgs
+    big = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
+    big.fill_(1)
+    red = torch.empty(2048 * 256, dtype=torch.int32, device=dev)
+
+    def read():
+        if lib.nf4_probe_read(big.data_ptr(), big.numel(), 2048, red.data_ptr(), s()):
+            raise RuntimeError("nf4_probe_read failed")
+    read_ms = best(read)
+    fill_ms = best(lambda: big.fill_(2))
+    del big
+    return {"mfma_tflops": round(flops / (mfma_ms * 1e-3) / 1e12, 1),
+            "hbm_read_gbps": round((4 << 30) / (read_ms * 1e-3) / 1e9, 1),
+            "hbm_write_gbps": round((4 << 30) / (fill_ms * 1e-3) / 1e9, 1),
+            "how": "nf4_probe_mfma (2048 workgroups x 4 waves x 4 accumulator chains of "
+                   "v_mfma_f32_32x32x16, N(0,1) operands), nf4_probe_read and torch fill_ over "
+                   "4 GiB; best of 3"}
+
+
+def mix_gbps(peaks, read_bytes, write_bytes):
+    """The measured HBM ceiling for a kernel moving read_bytes and write_bytes: the time the
+    measured read and write rates take for them, serially."""
+    t = read_bytes / peaks["hbm_read_gbps"] + write_bytes / peaks["hbm_write_gbps"]
+    return (read_bytes + write_bytes) / t
+
+
 # ------------------------------------------------------------------------------------- main
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_traffic_m2048.md"
@@ -613,6 +677,22 @@ def measured_traffic(kernel: str, dtype_name: str):
         if line.startswith("traffic_bytes_per_launch:"):
             vals = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
             return int(vals[kernel]) if kernel in vals else None
+    return None
+
+
+DEQUANT_TRAFFIC_PROFILE = ROOT / "profiles" / "dequant_table_traffic.md"
+
+
+def measured_dequant_traffic(dtype_name: str):
+    """HBM bytes per nf4_dequant_table launch over the 28-layer stack from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (fp16, calibrated against a copy of known size),
+    or None."""
+    if dtype_name != "f16" or not DEQUANT_TRAFFIC_PROFILE.exists():
+        return None
+    for line in DEQUANT_TRAFFIC_PROFILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            vals = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
+            return int(vals["dequant_table"]) if "dequant_table" in vals else None
     return None
 
 
@@ -688,11 +768,20 @@ def main():
         "gemm_only_tflops": round(gemm_tf, 2),
         "wall_s": round(wall, 3),
     }
+    peaks = measured_peaks(dtype, dev)
+    out["measured_peaks"] = peaks
+    out["mfma_peak_frac_measured"] = round(value / peaks["mfma_tflops"], 4)
+    out["roofline"]["peak_measured"] = peaks["mfma_tflops"]
+    out["roofline"]["frac_measured"] = round(achieved / peaks["mfma_tflops"], 4)
     if not args.no_dequant:
         dq = dequant_leg(dtype, dev)
+        bound = mix_gbps(peaks, dq["read_bytes"], dq["write_bytes"])
         out["dequant"] = dict(dq, roofline={"bound": "hbm", "achieved": dq["gbps"],
                                             "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                                            "frac": dq["frac"], "traffic": None})
+                                            "frac": dq["frac"],
+                                            "peak_measured": round(bound, 1),
+                                            "frac_measured": round(dq["gbps"] / bound, 4),
+                                            "traffic": measured_dequant_traffic(args.dtype)})
     if not args.no_swiglu:
         out.update(swiglu_leg(dtype, dev))
     if not args.no_int8 and args.dtype == "f16":
@@ -703,6 +792,10 @@ def main():
         out.update(varlen_stack_leg(dtype, dev, gemv=not args.no_gemv))
     if not args.no_7b:
         out.update(qwen7b_legs(dev, gemv=not args.no_gemv))
+    for leg in ("gemv_15b", "gemv_7b"):  # weight streaming: bounded by the measured read rate
+        for key, v in out.get(leg, {}).items():
+            if isinstance(v, dict) and "gbps" in v:
+                v["frac_measured"] = round(v["gbps"] / peaks["hbm_read_gbps"], 4)
     if args.copy_mib > 0:
         src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)

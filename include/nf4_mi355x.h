@@ -382,6 +382,20 @@ int nf4_swiglu_bwd(const void *grad, int64_t ld_h, const void *gate, const void 
 int nf4_bias_grad(const void *dy, int64_t m, int64_t n, int64_t lddy, float *out, int dtype,
                   void *stream);
 
+/* ------------------------------------------------------------------ measurement probes */
+
+/* No counterpart in the reference: measurements of what this device sustains, for the bench's
+ * fractions of measured peaks beside the data-sheet ones.
+ * nf4_probe_mfma: `workgroups` x 256 threads issue `iters` x 4 back-to-back
+ * v_mfma_f32_32x32x16 (dtype f16 or bf16) per wave on operands read from `operands` (>= 128
+ * 16-byte vectors), writing one float per thread to out (workgroups x 256 floats):
+ * 2 * 32 * 32 * 16 * 4 * iters * 4 * workgroups flops per launch.
+ * nf4_probe_read: reads `bytes` (a multiple of 16) from src with 16-byte loads over `workgroups`
+ * x 256 threads, writing one uint32 per thread to out. */
+int nf4_probe_mfma(const void *operands, int workgroups, int64_t iters, int dtype, float *out,
+                   void *stream);
+int nf4_probe_read(const void *src, int64_t bytes, int workgroups, uint32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
