@@ -98,6 +98,7 @@ struct GemmArgs {
     int vec_out;                  // 8-byte output stores allowed (paired: and aux loads)
     const uint16_t *aux;          // paired SwiGLU backward: dH [M, I]
     int64_t ld_aux;
+    int vec16_out;                // 16-byte output stores allowed (the LDS epilogue)
     int rows_groups;              // row-streaming path: row groups per workgroup
     int rows_parts;               // row-streaming path: K parts per row
 };
@@ -454,6 +455,84 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
                 }
             }
         }
+    }
+}
+
+// Epilogue of an unsplit 256-wide tile through LDS: the finished values are written to LDS in
+// the output's row-major layout, then stored as whole 16-byte chunks, 32 consecutive threads
+// per 512-byte tile row (+ bias, + the existing output when accumulating).  Stored straight
+// from the MFMA layout, each 8-byte store instruction would touch 32 output rows with 16 bytes
+// each (128 KB per 256x256 tile in 8192 pieces): measured 10-17 % of a K = 1536 launch, against
+// ~5 % this way.  LDS row m (one output row of the tile) holds its 256 columns as 32 chunks of 8
+// values, chunk c at position c ^ (m % 32), so the 32 rows one MFMA fragment's lanes write hit
+// distinct chunks.  Uses the staging LDS (BM x 512 bytes) after every wave's last fragment read.
+template <int DT, int BM, int TP, int TM, int NT>
+__device__ __forceinline__ void epilogue_lds(const GemmArgs &a, float16_t (&acc)[TP][TM],
+                                             uint8_t *lds, int64_t p0, int prow0, int64_t p_end,
+                                             int64_t col_off, int64_t m0, int mrow0) {
+    const int lane = threadIdx.x & 63;
+    __syncthreads();  // every wave's last fragment reads are done
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int m = mrow0 + j * 32 + (lane & 31);
+#pragma unroll
+        for (int i = 0; i < TP; ++i)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int p = prow0 + i * 32 + r4 * 8 + (lane >> 5) * 4;  // tile column
+                u32x2_t o;
+                o.x = pack2<DT>(acc[i][j][r4 * 4 + 0], acc[i][j][r4 * 4 + 1]);
+                o.y = pack2<DT>(acc[i][j][r4 * 4 + 2], acc[i][j][r4 * 4 + 3]);
+                const int c = (p >> 3) ^ (m & 31);
+                *reinterpret_cast<u32x2_t *>(lds + m * 512 + c * 16 + (p & 7) * 2) = o;
+            }
+    }
+    __syncthreads();
+    const int t = threadIdx.x % NT;
+    const int c = t & 31;  // the thread's chunk of a row: columns 8c .. 8c + 7
+#pragma unroll 4
+    for (int m = t >> 5; m < BM; m += NT / 32) {
+        const int64_t gm = m0 + m;
+        const int64_t p = p0 + 8 * c;
+        if (gm >= a.M || p >= p_end) continue;
+        u32x4_t v = *reinterpret_cast<const u32x4_t *>(lds + m * 512 + ((c ^ (m & 31)) << 4));
+        uint16_t *dst = static_cast<uint16_t *>(a.out) + gm * a.ld_out + col_off + p;
+        const bool whole = p + 8 <= p_end;
+        if (a.bias || a.accumulate || !whole) {
+            float f[8];
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f[2 * e] = to_f32<DT>(wv[e] & 0xffff);
+                f[2 * e + 1] = to_f32<DT>(wv[e] >> 16);
+            }
+            if (a.bias) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (p + e < p_end) f[e] += to_f32<DT>(a.bias[col_off + p + e]);
+            }
+            if (!whole) {
+                for (int e = 0; e < 8; ++e) {
+                    if (p + e >= p_end) break;
+                    float x = f[e];
+                    if (a.accumulate) x += to_f32<DT>(dst[e]);
+                    dst[e] = from_f32<DT>(x);
+                }
+                continue;
+            }
+            if (a.accumulate) {
+                const u32x4_t old = *reinterpret_cast<const u32x4_t *>(dst);
+                const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    f[2 * e] += to_f32<DT>(ow[e] & 0xffff);
+                    f[2 * e + 1] += to_f32<DT>(ow[e] >> 16);
+                }
+            }
+            v = (u32x4_t){pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]),
+                          pack2<DT>(f[6], f[7])};
+        }
+        *reinterpret_cast<u32x4_t *>(dst) = v;
     }
 }
 
@@ -883,12 +962,20 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
         if (v < nv) mma_step<DT, TP, TM, PH>(acc, sW[0], sA[0], prow0, wm * (BM / WM));
     }
     if constexpr (KG > 1) group_sum<TP, TM, KG, NT>(acc, &sT[0][0][0], g);
-    if constexpr (PAIR)
+    if constexpr (PAIR) {
         epilogue_swiglu<DT, TP, TM, EPI == 2, KG>(a, acc, p0 + prow0, a.w[0].rows,
                                                   m0 + wm * (BM / WM), g);
-    else
+    } else {
+        if constexpr (BP == 256 && KG == 1 && stage_bytes<BP, BM, KG>() >= BM * 512) {
+            if (a.vec16_out && bt.nsplit == 1) {
+                epilogue_lds<DT, BM, TP, TM, NT>(a, acc, lds, p0, prow0, w.rows, a.seg_off[seg],
+                                                 m0, wm * (BM / WM));
+                return;
+            }
+        }
         epilogue<DT, TP, TM, KG>(a, acc, p0 + prow0, w.rows, a.seg_off[seg], m0 + wm * (BM / WM),
                                  split, bt.nsplit > 1, g);
+    }
 }
 
 template <int DT, int BP, int BM, int WP, int WM, int EPI = 0, int KG = 1>
@@ -1610,6 +1697,13 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
                                         [](int) {});
     }
     if constexpr (KG > 1) group_sum<TP, TM, KG, NT>(acc, &sT[0][0][0], g);
+    if constexpr (BP == 256 && KG == 1 && stage_bytes<BP, BM, KG>() >= BM * 512) {
+        if (a.vec16_out && bt.nsplit == 1) {
+            epilogue_lds<DT, BM, TP, TM, NT>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
+                                             wm * (BM / WM));
+            return;
+        }
+    }
     epilogue<DT, TP, TM, KG>(a, acc, p0 + wp * (BP / WP), K, 0, m0 + wm * (BM / WM), split,
                              bt.nsplit > 1, g);
 }
@@ -2137,7 +2231,11 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
     g.ld_out = ldy;
     g.n_out = n_out;
     g.vec_out = aligned(y, 8) && ldy % 4 == 0;
-    for (int i = 0; i < nw; ++i) g.vec_out = g.vec_out && (g.seg_off[i] % 4 == 0);
+    g.vec16_out = aligned(y, 16) && ldy % 8 == 0;
+    for (int i = 0; i < nw; ++i) {
+        g.vec_out = g.vec_out && (g.seg_off[i] % 4 == 0);
+        g.vec16_out = g.vec16_out && (g.seg_off[i] % 8 == 0);
+    }
     bool lora_aligned = true;
     for (int i = 0; i < nlora; ++i)
         lora_aligned = lora_aligned && aligned(loras[i].b, 4) && aligned(loras[i].t, 4);
@@ -2249,6 +2347,7 @@ int linear_dx_impl(const void *dy, int64_t m, int64_t lddy, const nf4_weight *ws
     g.n_out = g.K;
     g.accumulate = accumulate != 0;
     g.vec_out = aligned(dx, 8) && lddx % 4 == 0;
+    g.vec16_out = aligned(dx, 16) && lddx % 8 == 0;
     const Plan p = plan_dx(m, ws, nw, tile, splits, ws_cap);
     if (p.splits == 0) return NF4_ERR_ARG;
     g.splits = p.splits;
