@@ -536,6 +536,55 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &a, float16_t (&acc)
     }
 }
 
+// The split-K partial sums of a 256-wide tile the same way, in fp32: the 256 x 256 tile is
+// 256 KB, so it goes through the staging LDS in two halves of 128 rows m (a wave's rows lie in
+// one half); LDS row m holds 256 floats as 64 chunks of 4, chunk c at c ^ (m % 32).
+template <int BM, int WM, int TP, int TM, int NT>
+__device__ __forceinline__ void partial_lds(const GemmArgs &a, float16_t (&acc)[TP][TM],
+                                            uint8_t *lds, int64_t p0, int prow0, int64_t p_end,
+                                            int64_t col_off, int64_t m0, int mrow0, int split) {
+    static_assert(BM % 128 == 0 && 128 % (BM / WM) == 0, "a wave's rows lie in one half");
+    const int lane = threadIdx.x & 63;
+    const int t = threadIdx.x % NT;
+    const int c = t & 63;  // the thread's chunk of a row: columns 4c .. 4c + 3
+#pragma unroll 1
+    for (int h = 0; h < BM / 128; ++h) {
+        __syncthreads();  // the staging tiles (h = 0) or the previous half's reads are done
+        if (mrow0 / 128 == h) {
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int m = mrow0 - 128 * h + j * 32 + (lane & 31);
+#pragma unroll
+                for (int i = 0; i < TP; ++i)
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        const int p = prow0 + i * 32 + r4 * 8 + (lane >> 5) * 4;
+                        const int cc = (p >> 2) ^ (m & 31);
+                        *reinterpret_cast<float4_t *>(lds + m * 1024 + cc * 16) =
+                            (float4_t){acc[i][j][r4 * 4 + 0], acc[i][j][r4 * 4 + 1],
+                                       acc[i][j][r4 * 4 + 2], acc[i][j][r4 * 4 + 3]};
+                    }
+            }
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int m = t >> 6; m < 128; m += NT / 64) {
+            const int64_t gm = m0 + 128 * h + m;
+            const int64_t p = p0 + 4 * c;
+            if (gm >= a.M || p >= p_end) continue;
+            const float4_t v = *reinterpret_cast<const float4_t *>(lds + m * 1024 + ((c ^ (m & 31)) << 4));
+            float *dst = a.partial + (static_cast<int64_t>(split) * a.M + gm) * a.tail_cols +
+                         (col_off + p - a.tail_col0);
+            if (p + 4 <= p_end) {
+                *reinterpret_cast<float4_t *>(dst) = v;
+            } else {
+                for (int e = 0; e < 4; ++e)
+                    if (p + e < p_end) dst[e] = v[e];
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------ weight tiles
 
 // Forward weight tile: BP rows x 64 k of W (natural layout).  Thread t owns 16 packed bytes =
@@ -970,6 +1019,11 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
             if (a.vec16_out && bt.nsplit == 1) {
                 epilogue_lds<DT, BM, TP, TM, NT>(a, acc, lds, p0, prow0, w.rows, a.seg_off[seg],
                                                  m0, wm * (BM / WM));
+                return;
+            }
+            if (bt.nsplit > 1 && a.tail_cols % 4 == 0 && (a.seg_off[seg] - a.tail_col0) % 4 == 0) {
+                partial_lds<BM, WM, TP, TM, NT>(a, acc, lds, p0, prow0, w.rows, a.seg_off[seg], m0,
+                                            wm * (BM / WM), split);
                 return;
             }
         }
@@ -1701,6 +1755,11 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
         if (a.vec16_out && bt.nsplit == 1) {
             epilogue_lds<DT, BM, TP, TM, NT>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
                                              wm * (BM / WM));
+            return;
+        }
+        if (bt.nsplit > 1 && a.tail_cols % 4 == 0 && a.tail_col0 % 4 == 0) {
+            partial_lds<BM, WM, TP, TM, NT>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
+                                        wm * (BM / WM), split);
             return;
         }
     }
