@@ -458,44 +458,61 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
     }
 }
 
-// Epilogue of an unsplit 256-wide tile through LDS: the finished values are written to LDS in
-// the output's row-major layout, then stored as whole 16-byte chunks, 32 consecutive threads
-// per 512-byte tile row (+ bias, + the existing output when accumulating).  Stored straight
+// Epilogue of an unsplit tile through LDS: the finished values are written to LDS in the
+// output's row-major layout, then stored as whole 16-byte chunks, one thread per chunk of a
+// tile row (+ bias, + the existing output when accumulating; with k-groups each group writes
+// the fragments it finished and every thread of the workgroup stores).  Stored straight
 // from the MFMA layout, each 8-byte store instruction would touch 32 output rows with 16 bytes
 // each (128 KB per 256x256 tile in 8192 pieces): measured 10-17 % of a K = 1536 launch, against
-// ~5 % this way.  LDS row m (one output row of the tile) holds its 256 columns as 32 chunks of 8
-// values, chunk c at position c ^ (m % 32), so the 32 rows one MFMA fragment's lanes write hit
-// distinct chunks.  Uses the staging LDS (BM x 512 bytes) after every wave's last fragment read.
-template <int DT, int BM, int TP, int TM, int NT>
+// ~5 % this way.  LDS row m (one output row of the tile) holds its BP columns as BP / 8 chunks of
+// 8 values, chunk c at position c ^ (m % min(32, BP / 8)), so the rows one MFMA fragment's lanes
+// write hit distinct chunks (two lanes per chunk for BP = 128).  Uses the staging LDS (BM x 2 BP
+// bytes) after every wave's last fragment read.
+template <int DT, int BP, int BM, int TP, int TM, int NT, int KG = 1>
 __device__ __forceinline__ void epilogue_lds(const GemmArgs &a, float16_t (&acc)[TP][TM],
                                              uint8_t *lds, int64_t p0, int prow0, int64_t p_end,
-                                             int64_t col_off, int64_t m0, int mrow0) {
+                                             int64_t col_off, int64_t m0, int mrow0, int g = 0) {
+    constexpr int RB = BP * 2;           // bytes of a tile row in LDS
+    constexpr int CPR = BP / 8;          // 16-byte chunks per row
+    constexpr int SW = CPR < 32 ? CPR : 32;
     const int lane = threadIdx.x & 63;
-    __syncthreads();  // every wave's last fragment reads are done
+    __syncthreads();  // every wave's last fragment reads (and k-group sums) are done
+    // Group g writes fragments j = KG jj + g.  The fragment is picked by selects rather than
+    // by a branch on g, which the compiler turns into dynamic indexing of acc (a copy of the
+    // accumulators in scratch memory).
 #pragma unroll
-    for (int j = 0; j < TM; ++j) {
-        const int m = mrow0 + j * 32 + (lane & 31);
+    for (int jj = 0; jj < TM / KG; ++jj) {
+        const int m = mrow0 + (jj * KG + g) * 32 + (lane & 31);
 #pragma unroll
-        for (int i = 0; i < TP; ++i)
+        for (int i = 0; i < TP; ++i) {
+            float16_t v = acc[i][jj * KG];
+#pragma unroll
+            for (int q = 1; q < KG; ++q)
+                if (g == q) v = acc[i][jj * KG + q];
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int p = prow0 + i * 32 + r4 * 8 + (lane >> 5) * 4;  // tile column
                 u32x2_t o;
-                o.x = pack2<DT>(acc[i][j][r4 * 4 + 0], acc[i][j][r4 * 4 + 1]);
-                o.y = pack2<DT>(acc[i][j][r4 * 4 + 2], acc[i][j][r4 * 4 + 3]);
-                const int c = (p >> 3) ^ (m & 31);
-                *reinterpret_cast<u32x2_t *>(lds + m * 512 + c * 16 + (p & 7) * 2) = o;
+                o.x = pack2<DT>(v[r4 * 4 + 0], v[r4 * 4 + 1]);
+                o.y = pack2<DT>(v[r4 * 4 + 2], v[r4 * 4 + 3]);
+                const int c = (p >> 3) ^ (m & (SW - 1));
+                *reinterpret_cast<u32x2_t *>(lds + m * RB + c * 16 + (p & 7) * 2) = o;
             }
+        }
     }
     __syncthreads();
-    const int t = threadIdx.x % NT;
-    const int c = t & 31;  // the thread's chunk of a row: columns 8c .. 8c + 7
+    constexpr int NTA = KG * NT;  // every thread of the workgroup stores
+    const int t = threadIdx.x % NTA;
+    const int c = t % CPR;  // the thread's chunk of a row: columns 8c .. 8c + 7
+    constexpr int RSTEP = NTA / CPR;  // tile rows stored per pass
+    static_assert(BM % RSTEP == 0, "whole passes over the tile rows");
 #pragma unroll 4
-    for (int m = t >> 5; m < BM; m += NT / 32) {
+    for (int it = 0; it < BM / RSTEP; ++it) {
+        const int m = t / CPR + it * RSTEP;
         const int64_t gm = m0 + m;
         const int64_t p = p0 + 8 * c;
         if (gm >= a.M || p >= p_end) continue;
-        u32x4_t v = *reinterpret_cast<const u32x4_t *>(lds + m * 512 + ((c ^ (m & 31)) << 4));
+        u32x4_t v = *reinterpret_cast<const u32x4_t *>(lds + m * RB + ((c ^ (m & (SW - 1))) << 4));
         uint16_t *dst = static_cast<uint16_t *>(a.out) + gm * a.ld_out + col_off + p;
         const bool whole = p + 8 <= p_end;
         if (a.bias || a.accumulate || !whole) {
@@ -512,11 +529,13 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &a, float16_t (&acc)
                     if (p + e < p_end) f[e] += to_f32<DT>(a.bias[col_off + p + e]);
             }
             if (!whole) {
-                for (int e = 0; e < 8; ++e) {
-                    if (p + e >= p_end) break;
-                    float x = f[e];
-                    if (a.accumulate) x += to_f32<DT>(dst[e]);
-                    dst[e] = from_f32<DT>(x);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {  // unrolled: f stays in registers
+                    if (p + e < p_end) {
+                        float x = f[e];
+                        if (a.accumulate) x += to_f32<DT>(dst[e]);
+                        dst[e] = from_f32<DT>(x);
+                    }
                 }
                 continue;
             }
@@ -1015,12 +1034,14 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
         epilogue_swiglu<DT, TP, TM, EPI == 2, KG>(a, acc, p0 + prow0, a.w[0].rows,
                                                   m0 + wm * (BM / WM), g);
     } else {
-        if constexpr (BP == 256 && KG == 1 && stage_bytes<BP, BM, KG>() >= BM * 512) {
+        if constexpr (stage_bytes<BP, BM, KG>() >= BM * BP * 2) {
             if (a.vec16_out && bt.nsplit == 1) {
-                epilogue_lds<DT, BM, TP, TM, NT>(a, acc, lds, p0, prow0, w.rows, a.seg_off[seg],
-                                                 m0, wm * (BM / WM));
+                epilogue_lds<DT, BP, BM, TP, TM, NT, KG>(a, acc, lds, p0, prow0, w.rows,
+                                                         a.seg_off[seg], m0, wm * (BM / WM), g);
                 return;
             }
+        }
+        if constexpr (BP == 256 && KG == 1 && stage_bytes<BP, BM, KG>() >= BM * 512) {
             if (bt.nsplit > 1 && a.tail_cols % 4 == 0 && (a.seg_off[seg] - a.tail_col0) % 4 == 0) {
                 partial_lds<BM, WM, TP, TM, NT>(a, acc, lds, p0, prow0, w.rows, a.seg_off[seg], m0,
                                             wm * (BM / WM), split);
@@ -1751,12 +1772,14 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
                                         [](int) {});
     }
     if constexpr (KG > 1) group_sum<TP, TM, KG, NT>(acc, &sT[0][0][0], g);
-    if constexpr (BP == 256 && KG == 1 && stage_bytes<BP, BM, KG>() >= BM * 512) {
+    if constexpr (stage_bytes<BP, BM, KG>() >= BM * BP * 2) {
         if (a.vec16_out && bt.nsplit == 1) {
-            epilogue_lds<DT, BM, TP, TM, NT>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
-                                             wm * (BM / WM));
+            epilogue_lds<DT, BP, BM, TP, TM, NT, KG>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
+                                                     wm * (BM / WM), g);
             return;
         }
+    }
+    if constexpr (BP == 256 && KG == 1 && stage_bytes<BP, BM, KG>() >= BM * 512) {
         if (bt.nsplit > 1 && a.tail_cols % 4 == 0 && a.tail_col0 % 4 == 0) {
             partial_lds<BM, WM, TP, TM, NT>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
                                         wm * (BM / WM), split);
