@@ -17,6 +17,12 @@ __device__ __forceinline__ float ld1(const uint16_t *p) {
 }
 
 template <int DT>
+__device__ __forceinline__ float bits_f32(uint32_t v) {  // low 16 bits of v
+    if constexpr (DT == NF4_BF16) return __uint_as_float(v << 16);
+    else return static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(v)));
+}
+
+template <int DT>
 __device__ __forceinline__ uint16_t st1(float v) {
     return round16<DT>(v);
 }
@@ -350,18 +356,60 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint16_t *grad, i
     }
 }
 
-// Column sums of dY, two passes like the LoRA weight gradients (rank 1, V = 1).
+// Column sums of dY [M, N] in one pass: a workgroup owns kColsumCols = 64 columns; thread t
+// takes 8 of them (chunk t % 8: one 16-byte load per row when `vec`) and the rows r with
+// r % 32 == t / 8, in increasing order, 8 rows' loads in flight; the 32 row-lane sums of a
+// column are then added in row-lane order through LDS (deterministic).
+constexpr int kColsumCols = 64;
 template <int DT>
-__global__ __launch_bounds__(256) void colsum_partial_kernel(const uint16_t *dy, int64_t m, int64_t n,
-                                                             int64_t ld, int64_t rows_per_chunk,
-                                                             float *part) {
-    const int64_t col = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows_per_chunk;
-    const int64_t r1 = r0 + rows_per_chunk < m ? r0 + rows_per_chunk : m;
-    if (col >= n) return;
-    float s = 0.f;
-    for (int64_t r = r0; r < r1; ++r) s += ld1<DT>(dy + r * ld + col);
-    part[blockIdx.y * n + col] = s;
+__global__ __launch_bounds__(256) void colsum_kernel(const uint16_t *dy, int64_t m, int64_t n,
+                                                     int64_t ld, int vec, float *out) {
+    __shared__ float s_part[32][kColsumCols + 1];
+    const int t = threadIdx.x, cq = t & 7, rl = t >> 3;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kColsumCols + cq * 8;
+    const int nc = n - c0 >= 8 ? 8 : (n - c0 > 0 ? static_cast<int>(n - c0) : 0);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t r = rl;
+    if (vec && nc == 8) {
+        for (; r + 7 * 32 < m; r += 8 * 32) {
+            u32x4_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = *reinterpret_cast<const u32x4_t *>(dy + (r + u * 32) * ld + c0);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[2 * e] += bits_f32<DT>(w[e] & 0xffff);
+                    acc[2 * e + 1] += bits_f32<DT>(w[e] >> 16);
+                }
+            }
+        }
+        for (; r < m; r += 32) {
+            const u32x4_t v = *reinterpret_cast<const u32x4_t *>(dy + r * ld + c0);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[2 * e] += bits_f32<DT>(w[e] & 0xffff);
+                acc[2 * e + 1] += bits_f32<DT>(w[e] >> 16);
+            }
+        }
+    } else {
+        for (; r < m; r += 32)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (e < nc) acc[e] += ld1<DT>(dy + r * ld + c0 + e);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_part[rl][cq * 8 + e] = acc[e];
+    __syncthreads();
+    if (t < kColsumCols) {
+        const int64_t c = static_cast<int64_t>(blockIdx.x) * kColsumCols + t;
+        float sum = 0.f;
+        for (int i = 0; i < 32; ++i) sum += s_part[i][t];
+        if (c < n) out[c] = sum;
+    }
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(float *out, int64_t n) {
@@ -667,14 +715,14 @@ extern "C" int nf4_bias_grad(const void *dy, int64_t m, int64_t n, int64_t lddy,
         return status_of(hipGetLastError());
     }
     if (!dy || lddy < n) return NF4_ERR_ARG;
-    // One pass with a single chunk per column keeps this workspace-free: a thread per column,
-    // rows in order (deterministic).
-    const dim3 grid(static_cast<unsigned>((n + 255) / 256), 1);
+    // Workspace-free and deterministic: a workgroup per 64 columns, rows split over its threads
+    // in a fixed way and the row-lane sums added in order.
+    const int vec = n % 8 == 0 && lddy % 8 == 0 && aligned(dy, 16);
+    const dim3 grid(static_cast<unsigned>((n + kColsumCols - 1) / kColsumCols));
+    const auto d = static_cast<const uint16_t *>(dy);
     if (dtype == NF4_BF16)
-        hipLaunchKernelGGL(colsum_partial_kernel<NF4_BF16>, grid, dim3(256), 0, s,
-                           static_cast<const uint16_t *>(dy), m, n, lddy, m, out);
+        hipLaunchKernelGGL(colsum_kernel<NF4_BF16>, grid, dim3(256), 0, s, d, m, n, lddy, vec, out);
     else
-        hipLaunchKernelGGL(colsum_partial_kernel<NF4_F16>, grid, dim3(256), 0, s,
-                           static_cast<const uint16_t *>(dy), m, n, lddy, m, out);
+        hipLaunchKernelGGL(colsum_kernel<NF4_F16>, grid, dim3(256), 0, s, d, m, n, lddy, vec, out);
     return status_of(hipGetLastError());
 }

@@ -192,6 +192,29 @@ def test_bias_grad_and_swiglu(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,n,pad", [(0, 64, 0), (1, 8, 0), (37, 100, 0), (2048, 2048, 0),
+                                     (5000, 264, 0), (300, 96, 3), (257, 2048, 8)])
+def test_bias_grad_shapes(cuda, m, n, pad, dtype):
+    """nf4_bias_grad (the column sum of nf4.py:100-101) on the 16-byte path (n and the row
+    pitch multiples of 8) and the element path (n = 100, pitch n + 3), M = 0 and M beyond one
+    row lane's stride; deterministic (two calls bit-equal).  fp32 sums in a fixed order: the
+    error against the fp64 sum stays below 2e-5 of the column's absolute sum."""
+    from solution import kernels
+
+    banner(f"bias grad m={m} n={n} pad={pad} {dtype}")
+    g = torch.Generator().manual_seed(m * 7 + n)
+    full = (torch.randn(m, n + pad, generator=g) * 0.1).to(dtype)
+    dy = full.to(cuda)[:, :n]
+    got = kernels.bias_grad(dy)
+    again = kernels.bias_grad(dy)
+    assert torch.equal(got, again)
+    ref = full[:, :n].double().sum(0)
+    bound = 2e-5 * full[:, :n].double().abs().sum(0) + 1e-30
+    err = (got.cpu().double() - ref).abs()
+    assert bool((err <= bound).all()), float((err / bound).max())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [1, 8, 33, 64])
 def test_small_m_stacked_bias_lora(cuda, m, dtype):
     """The small-M forward path (decode regime): stacked segments whose row counts are not
