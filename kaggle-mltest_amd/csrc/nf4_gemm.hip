@@ -1876,12 +1876,11 @@ struct Plan {
     int64_t blocks() const { return tail_start + (tiles - tail_start) * splits; }
 };
 
-// The small-M forward path takes M <= kGemvMaxM (32 x 1 or 2 activation rows per MFMA
-// B operand).  Its workgroups own 32 weight rows and their share of the reduction, spread over
+// The small-M forward path takes M <= kGemvMaxM (32 activation rows: one MFMA B operand).  Its workgroups own 32 weight rows and their share of the reduction, spread over
 // 16 waves (8 with two activation fragments) while there are at most as many workgroups as
 // CUs, else 4 waves with several steps each.  Long reductions over few row tiles are split over
 // workgroups.
-constexpr int64_t kGemvMaxM = 64;
+constexpr int64_t kGemvMaxM = 32;
 
 constexpr int kCUs = 256;
 
@@ -2016,10 +2015,8 @@ Plan plan_gemv(int64_t m, const nf4_weight *ws, int nw) {
     int64_t tiles = 0;
     for (int i = 0; i < nw; ++i) tiles += (ws[i].rows + 31) / 32;
     const int64_t steps = ws[0].cols / BR;
-    const int mt = m <= 32 ? 1 : 2;
     int waves = tiles > kCUs ? 4 : 16;
     while (waves > 4 && waves > steps) waves /= 2;
-    if (mt == 2 && waves > 8) waves = 8;  // two activation fragments need more than 128 VGPRs
     // few row tiles and a long reduction: split it over workgroups (fp32 partials + the
     // fixed-order reduction) so that more CUs dequantize, keeping >= 2 steps per wave
     int64_t splits = 1;
@@ -2031,7 +2028,7 @@ Plan plan_gemv(int64_t m, const nf4_weight *ws, int nw) {
         if (splits < 1) splits = 1;
         while (splits > 1 && (splits - 1) * ((steps + splits - 1) / splits) >= steps) --splits;
     }
-    return Plan{2, 32, 32 * mt, static_cast<int>(splits), tiles, waves, splits > 1 ? 0 : tiles};
+    return Plan{2, 32, 32, static_cast<int>(splits), tiles, waves, splits > 1 ? 0 : tiles};
 }
 
 // Decode path: waves per 16-row tile, the most (up to 8) that keep the whole launch resident
@@ -2048,10 +2045,10 @@ Plan plan_decode(const nf4_weight *ws, int nw) {
 }
 
 // Forward path by token count: the decode kernel up to 16 tokens (K a multiple of 128), the
-// small-M kernel up to 32, and from 33 to 64 the small-M kernel only for long reductions over
-// few rows (sum of rows < K); the tiled GEMMs otherwise (measured at M = 64 on the Qwen2.5-1.5B
-// and -7B projections: q|k|v, o and gate|up 4-30 % faster tiled with split-K, the 1.5B down
-// projection 25 % faster on the small-M kernel).
+// small-M kernel up to 32, the tiled GEMMs (with split-K) from 33 on.  Measured on 4-layer
+// Qwen2.5-1.5B / -7B stacks (forward per layer, HIP graph replay): at M = 20-32 the small-M
+// kernel is 10-22 % faster on the 1.5B stack and within -6..+6 % on the 7B stack; at M = 40-64
+// the tiled plans are up to 12 % faster per layer (the 7B down projection, K = 18944, most).
 // A tiling pinned by the caller: tile shape `tile` (0, 1 or 3 as Plan::cfg) with every tile's
 // reduction split `splits` ways (1: none); an empty last split is refused (splits = 0 returned).
 Plan pinned_plan(int tile, int splits, int64_t big, int64_t small, int64_t steps) {
@@ -2107,11 +2104,7 @@ Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits
               bool rows_allowed = true) {
     if (tile < 0 && rows_allowed && rows_ok(m, ws, nw)) return plan_rows(m, ws, nw);
     if (tile < 0 && m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
-    if (tile < 0 && m <= kGemvMaxM) {
-        int64_t n = 0;
-        for (int i = 0; i < nw; ++i) n += ws[i].rows;
-        if (m <= 32 || n < ws[0].cols) return plan_gemv(m, ws, nw);
-    }
+    if (tile < 0 && m <= kGemvMaxM) return plan_gemv(m, ws, nw);
     int64_t big = 0, small = 0;
     for (int i = 0; i < nw; ++i) {
         big += (ws[i].rows + 255) / 256;
@@ -2145,14 +2138,9 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
         else hipLaunchKernelGGL((decode_kernel<DT, 1>), grid, block, 0, st, g);
     } else if (p.cfg == 2) {
         const dim3 block(p.waves * 64);
-        if (p.bm == 32) {
-            if (p.waves == 16) hipLaunchKernelGGL((gemv_kernel<DT, 1, 16>), grid, block, 0, st, g);
-            else if (p.waves == 8) hipLaunchKernelGGL((gemv_kernel<DT, 1, 8>), grid, block, 0, st, g);
-            else hipLaunchKernelGGL((gemv_kernel<DT, 1, 4>), grid, block, 0, st, g);
-        } else {
-            if (p.waves >= 8) hipLaunchKernelGGL((gemv_kernel<DT, 2, 8>), grid, dim3(512), 0, st, g);
-            else hipLaunchKernelGGL((gemv_kernel<DT, 2, 4>), grid, block, 0, st, g);
-        }
+        if (p.waves == 16) hipLaunchKernelGGL((gemv_kernel<DT, 1, 16>), grid, block, 0, st, g);
+        else if (p.waves == 8) hipLaunchKernelGGL((gemv_kernel<DT, 1, 8>), grid, block, 0, st, g);
+        else hipLaunchKernelGGL((gemv_kernel<DT, 1, 4>), grid, block, 0, st, g);
     } else if (p.cfg == 0)
         hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
     else if (p.cfg == 3)
