@@ -458,10 +458,11 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
     }
 }
 
-// Epilogue of an unsplit tile through LDS: the finished values are written to LDS in the
-// output's row-major layout, then stored as whole 16-byte chunks, one thread per chunk of a
-// tile row (+ bias, + the existing output when accumulating; with k-groups each group writes
-// the fragments it finished and every thread of the workgroup stores).  Stored straight
+// Epilogue of an unsplit tile without a bias or an accumulated output through LDS: the
+// finished values are rounded to the output dtype and written to LDS in the output's row-major
+// layout, then stored as whole 16-byte chunks, one thread per chunk of a tile row (with
+// k-groups each group writes the fragments it finished and every thread of the workgroup
+// stores).  Stored straight
 // from the MFMA layout, each 8-byte store instruction would touch 32 output rows with 16 bytes
 // each (128 KB per 256x256 tile in 8192 pieces): measured 10-17 % of a K = 1536 launch, against
 // ~5 % this way.  LDS row m (one output row of the tile) holds its BP columns as BP / 8 chunks of
@@ -514,44 +515,93 @@ __device__ __forceinline__ void epilogue_lds(const GemmArgs &a, float16_t (&acc)
         if (gm >= a.M || p >= p_end) continue;
         u32x4_t v = *reinterpret_cast<const u32x4_t *>(lds + m * RB + ((c ^ (m & (SW - 1))) << 4));
         uint16_t *dst = static_cast<uint16_t *>(a.out) + gm * a.ld_out + col_off + p;
-        const bool whole = p + 8 <= p_end;
-        if (a.bias || a.accumulate || !whole) {
-            float f[8];
+        if (p + 8 > p_end) {  // the last, partial chunk of a row
             const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                f[2 * e] = to_f32<DT>(wv[e] & 0xffff);
-                f[2 * e + 1] = to_f32<DT>(wv[e] >> 16);
-            }
-            if (a.bias) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (p + e < p_end) f[e] += to_f32<DT>(a.bias[col_off + p + e]);
-            }
-            if (!whole) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {  // unrolled: f stays in registers
-                    if (p + e < p_end) {
-                        float x = f[e];
-                        if (a.accumulate) x += to_f32<DT>(dst[e]);
-                        dst[e] = from_f32<DT>(x);
-                    }
-                }
-                continue;
-            }
-            if (a.accumulate) {
-                const u32x4_t old = *reinterpret_cast<const u32x4_t *>(dst);
-                const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    f[2 * e] += to_f32<DT>(ow[e] & 0xffff);
-                    f[2 * e + 1] += to_f32<DT>(ow[e] >> 16);
-                }
-            }
-            v = (u32x4_t){pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]),
-                          pack2<DT>(f[6], f[7])};
+            for (int e = 0; e < 8; ++e)
+                if (p + e < p_end) dst[e] = static_cast<uint16_t>(wv[e >> 1] >> ((e & 1) * 16));
+            continue;
         }
         *reinterpret_cast<u32x4_t *>(dst) = v;
+    }
+}
+
+// epilogue_lds for tiles with a bias or an accumulated output: the accumulators go to LDS as
+// fp32 (BM x BP x 4 bytes, chunk cc = 4 columns of row m at cc ^ (m % 32)), and the bias and
+// the existing output are added in fp32 before the one rounding, in the order of the
+// register epilogue (bit-identical to it).  Each thread's 8 columns are the same on every row
+// it stores, so it loads their bias once.
+template <int DT, int BP, int BM, int TP, int TM, int NT, int KG = 1>
+__device__ __forceinline__ void epilogue_lds32(const GemmArgs &a, float16_t (&acc)[TP][TM],
+                                               uint8_t *lds, int64_t p0, int prow0, int64_t p_end,
+                                               int64_t col_off, int64_t m0, int mrow0, int g = 0) {
+    static_assert(BP / 4 == 32, "32 four-column chunks per LDS row");
+    constexpr int RB = BP * 4;
+    const int lane = threadIdx.x & 63;
+    __syncthreads();  // every wave's last fragment reads (and k-group sums) are done
+#pragma unroll
+    for (int jj = 0; jj < TM / KG; ++jj) {
+        const int m = mrow0 + (jj * KG + g) * 32 + (lane & 31);
+#pragma unroll
+        for (int i = 0; i < TP; ++i) {
+            float16_t v = acc[i][jj * KG];
+#pragma unroll
+            for (int q = 1; q < KG; ++q)
+                if (g == q) v = acc[i][jj * KG + q];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int p = prow0 + i * 32 + r4 * 8 + (lane >> 5) * 4;
+                *reinterpret_cast<float4_t *>(lds + m * RB + (((p >> 2) ^ (m & 31)) << 4)) =
+                    (float4_t){v[r4 * 4], v[r4 * 4 + 1], v[r4 * 4 + 2], v[r4 * 4 + 3]};
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int NTA = KG * NT;
+    constexpr int CPR = BP / 8;
+    const int t = threadIdx.x % NTA;
+    const int c = t % CPR;  // columns 8c .. 8c + 7: LDS chunks 2c and 2c + 1
+    const int64_t p = p0 + 8 * c;
+    float bf[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        bf[e] = (a.bias && p + e < p_end) ? to_f32<DT>(a.bias[col_off + p + e]) : 0.0f;
+    constexpr int RSTEP = NTA / CPR;
+    static_assert(BM % RSTEP == 0, "whole passes over the tile rows");
+#pragma unroll 2
+    for (int it = 0; it < BM / RSTEP; ++it) {
+        const int m = t / CPR + it * RSTEP;
+        const int64_t gm = m0 + m;
+        if (gm >= a.M || p >= p_end) continue;
+        const float4_t lo4 = *reinterpret_cast<const float4_t *>(lds + m * RB + (((2 * c) ^ (m & 31)) << 4));
+        const float4_t hi4 = *reinterpret_cast<const float4_t *>(lds + m * RB + (((2 * c + 1) ^ (m & 31)) << 4));
+        float f[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+        if (a.bias) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] += bf[e];
+        }
+        uint16_t *dst = static_cast<uint16_t *>(a.out) + gm * a.ld_out + col_off + p;
+        if (p + 8 > p_end) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (p + e < p_end) {
+                    float x = f[e];
+                    if (a.accumulate) x += to_f32<DT>(dst[e]);
+                    dst[e] = from_f32<DT>(x);
+                }
+            continue;
+        }
+        if (a.accumulate) {
+            const u32x4_t old = *reinterpret_cast<const u32x4_t *>(dst);
+            const uint32_t ow[4] = {old.x, old.y, old.z, old.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f[2 * e] += to_f32<DT>(ow[e] & 0xffff);
+                f[2 * e + 1] += to_f32<DT>(ow[e] >> 16);
+            }
+        }
+        *reinterpret_cast<u32x4_t *>(dst) = (u32x4_t){pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]),
+                                                      pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
     }
 }
 
@@ -1035,9 +1085,16 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
                                                   m0 + wm * (BM / WM), g);
     } else {
         if constexpr (stage_bytes<BP, BM, KG>() >= BM * BP * 2) {
-            if (a.vec16_out && bt.nsplit == 1) {
+            if (a.vec16_out && bt.nsplit == 1 && !a.bias && !a.accumulate) {
                 epilogue_lds<DT, BP, BM, TP, TM, NT, KG>(a, acc, lds, p0, prow0, w.rows,
                                                          a.seg_off[seg], m0, wm * (BM / WM), g);
+                return;
+            }
+        }
+        if constexpr (BP == 128 && stage_bytes<BP, BM, KG>() >= BM * BP * 4) {
+            if (a.vec16_out && bt.nsplit == 1) {
+                epilogue_lds32<DT, BP, BM, TP, TM, NT, KG>(a, acc, lds, p0, prow0, w.rows,
+                                                           a.seg_off[seg], m0, wm * (BM / WM), g);
                 return;
             }
         }
@@ -1773,9 +1830,16 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
     }
     if constexpr (KG > 1) group_sum<TP, TM, KG, NT>(acc, &sT[0][0][0], g);
     if constexpr (stage_bytes<BP, BM, KG>() >= BM * BP * 2) {
-        if (a.vec16_out && bt.nsplit == 1) {
+        if (a.vec16_out && bt.nsplit == 1 && !a.bias && !a.accumulate) {
             epilogue_lds<DT, BP, BM, TP, TM, NT, KG>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
                                                      wm * (BM / WM), g);
+            return;
+        }
+    }
+    if constexpr (BP == 128 && stage_bytes<BP, BM, KG>() >= BM * BP * 4) {
+        if (a.vec16_out && bt.nsplit == 1) {
+            epilogue_lds32<DT, BP, BM, TP, TM, NT, KG>(a, acc, lds, p0, wp * (BP / WP), K, 0, m0,
+                                                       wm * (BM / WM), g);
             return;
         }
     }

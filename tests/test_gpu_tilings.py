@@ -150,3 +150,34 @@ def test_head_tail_plans_bit_exact(cuda):
     dy[torch.arange(m), torch.arange(m) % k] = 1.0
     dx = kernels.linear_dx(dy, [down]).cpu().view(torch.int16)
     assert torch.equal(dx, wd[torch.arange(m) % k])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("tile", TILES)
+def test_lds_epilogue_matches_register_epilogue(cuda, tile, dtype):
+    """The epilogues that stage a finished tile through LDS (16-byte row stores; in fp32 when a
+    bias is added or the output accumulates, so the result is rounded once) against the
+    register epilogue that writes from the MFMA layout, which runs when the output rows are
+    not 16-byte aligned.  Same plan, same accumulators: outputs bit-equal, forward with a bias
+    and input gradient with accumulation, a partial last 8-column chunk included (N = 1000)."""
+    from solution import kernels
+
+    banner(f"LDS epilogue vs register epilogue tile={tile} {dtype}")
+    m, k = 300, 320
+    segs = [random_weight(n, k, seed=500 + n, dev=cuda) for n in (1000, 256)]
+    n = 1256
+    x = _x(m, k, 51, cuda, dtype)
+    bias = _x(1, n, 52, cuda, dtype).view(-1)
+    y_al = torch.empty(m, n, dtype=dtype, device=cuda)
+    y_mis = torch.empty(m * n + 8, dtype=dtype, device=cuda)[1:1 + m * n].view(m, n)
+    kernels.linear_fwd(x, segs, bias, out=y_al, tile=tile)
+    kernels.linear_fwd(x, segs, bias, out=y_mis, tile=tile)
+    assert torch.equal(y_al, y_mis)
+    dy = _x(m, n, 53, cuda, dtype, std=1e-2)
+    base = _x(m, k, 54, cuda, dtype)
+    d_al = base.clone()
+    d_mis = torch.empty(m * k + 8, dtype=dtype, device=cuda)[1:1 + m * k].view(m, k)
+    d_mis.copy_(base)
+    kernels.linear_dx(dy, segs, out=d_al, accumulate=True, tile=tile)
+    kernels.linear_dx(dy, segs, out=d_mis, accumulate=True, tile=tile)
+    assert torch.equal(d_al, d_mis)
