@@ -401,21 +401,29 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
                                          int64_t p_base, int64_t p_end, int64_t col_off,
                                          int64_t m_base, int split, bool to_partial, int g = 0) {
     const int lane = threadIdx.x & 63;
+    // fragments j inside (i, r4): a lane's columns are the same in every j, so their bias is
+    // loaded once per (i, r4)
 #pragma unroll
-    for (int j = 0; j < TM; ++j) {
-        if (KG > 1 && j % KG != g) continue;  // another k-group's fragments
-        const int64_t m = m_base + j * 32 + (lane & 31);
-        if (m >= a.M) continue;
+    for (int i = 0; i < TP; ++i) {
 #pragma unroll
-        for (int i = 0; i < TP; ++i) {
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int64_t p = p_base + i * 32 + r4 * 8 + (lane >> 5) * 4;
+            if (p >= p_end) continue;
+            const int64_t col = col_off + p;
+            const bool full = p + 4 <= p_end;
+            float bv[4] = {0.f, 0.f, 0.f, 0.f};
+            if (a.bias && !to_partial) {
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int64_t p = p_base + i * 32 + r4 * 8 + (lane >> 5) * 4;
-                if (p >= p_end) continue;
-                const int64_t col = col_off + p;
+                for (int q = 0; q < 4; ++q)
+                    if (p + q < p_end) bv[q] = to_f32<DT>(a.bias[col + q]);
+            }
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                if (KG > 1 && j % KG != g) continue;  // another k-group's fragments
+                const int64_t m = m_base + j * 32 + (lane & 31);
+                if (m >= a.M) continue;
                 float v[4] = {acc[i][j][r4 * 4 + 0], acc[i][j][r4 * 4 + 1],
                               acc[i][j][r4 * 4 + 2], acc[i][j][r4 * 4 + 3]};
-                const bool full = p + 4 <= p_end;
                 if (to_partial) {
                     float *dst = a.partial + (static_cast<int64_t>(split) * a.M + m) * a.tail_cols +
                                  (col - a.tail_col0);
@@ -430,8 +438,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs &a, float16_t (&acc)[TP]
                 uint16_t *dst = static_cast<uint16_t *>(a.out) + m * a.ld_out + col;
                 if (a.bias) {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (p + q < p_end) v[q] += to_f32<DT>(a.bias[col + q]);
+                    for (int q = 0; q < 4; ++q) v[q] += bv[q];
                 }
                 if (full && a.vec_out) {
                     if (a.accumulate) {
