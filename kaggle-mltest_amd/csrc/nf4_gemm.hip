@@ -1299,8 +1299,8 @@ void decode_kernel(const GemmArgs a) {
 
 // ------------------------------------------------------------------- small-M forward path
 //
-// Y = X W^T for M <= 32 * MT tokens, MT 1 or 2 (the decode regime), bound by reading the packed
-// weights.  A workgroup owns 32 weight rows of one segment; its NW waves split the reduction,
+// Y = X W^T for M <= 32 * MT tokens (the decode regime; the planner launches MT = 1 only, the
+// tiled GEMMs being faster from 33 tokens on), bound by reading the packed weights.  A workgroup owns 32 weight rows of one segment; its NW waves split the reduction,
 // each dequantizing its rows straight into MFMA A-fragment registers (no LDS staging) and
 // reading its activation B-fragments from global memory (rows >= M read as zero from the
 // buffer range check).  Inside a 64-deep step both operands use the same k order: lane half h
