@@ -1461,16 +1461,27 @@ void gemv_kernel(const GemmArgs a) {
 //
 // Y = X W^T for M <= 2 tokens: bound by reading the packed weight once.  A row is cut into 1 KB
 // slots of packed bytes (2048 k; lane l of a wave takes the 16 bytes at 16 l, 32 elements inside
-// one absmax block) and the slots into K parts of SP <= 2 slots.  A wave owns one K part of up
-// to kRowsMaxRows consecutive rows of one segment and keeps its part's activations (64 bytes per
-// lane, slot and token) in registers for all of them, so the main loop streams weight bytes
-// only.  A constant 256-entry LDS table maps a packed byte to its two codes rounded to the GEMM
-// dtype as one pair (code[high nibble] in the low half: element order): a packed byte is one
-// table read and, per token, one v_dot2 with the activation pair, accumulated in fp32, and a
-// lane's 32 products are then scaled by their block's fp32 absmax (rebuilt as in the other
-// kernels).  The numerics are those of bitsandbytes' decode GEMV (no fp16 weight is formed)
-// except that the 16 codes are rounded to the GEMM dtype: each product is round16(code[nib]) * x
-// exactly and a block's sum is scaled by its absmax in fp32.
+// one absmax block) and the slots into K parts of SP <= 2 slots.  A row group owns up to
+// kRowsMaxRows rows of one segment, interleaved over the segment's groups (group g takes rows
+// g, g + G, g + 2G, .. of the segment's G groups, so that at any time the launch reads one
+// contiguous stretch of the weight: measured 2 % faster than consecutive rows per group); a
+// wave owns one K part of its group's rows and keeps the part's activations (64 bytes per lane,
+// slot and token) in registers for all of them, so the main loop streams weight bytes only.
+// An LDS table maps a packed byte to its two codes rounded to the GEMM dtype as one pair
+// (code[high nibble] in the low half: element order): a packed byte is one table read and, per
+// token, one v_dot2 with the activation pair, accumulated in fp32, and a lane's 32 products are
+// then scaled by their block's fp32 absmax (rebuilt as in the other kernels).  The numerics are
+// those of bitsandbytes' decode GEMV (no fp16 weight is formed) except that the 16 codes are
+// rounded to the GEMM dtype: each product is round16(code[nib]) * x exactly and a block's sum is
+// scaled by its absmax in fp32.
+//
+// The table: with one slot per part (K <= 2048) one 1 KB copy; random bytes make its reads
+// ~4-way bank conflicted (the LDS is busy ~5 cycles per read), which the short launches of
+// such rows do not feel.  With two slots per part, 64 copies, entry e of copy l at dword
+// 64 e + l, so that lane l reads only bank l (no conflicts; the byte address 256 e + 4 l is one
+// v_perm of the packed dword and 4 l) and 16-wave workgroups (one per CU) to amortize its 64 KB
+// fill: the 7B gate|up and down projections at M = 1 measured 15-18 % faster with it, the
+// one-slot 1.5B launches up to 40 % slower (the fill does not pay for itself there).
 //
 // After each row the lane partials are reduced across the wave in a fixed order (DPP within
 // rows of 16 lanes, then the four rows) and lane r keeps the sum of the wave's row r.  Rows with
@@ -1489,16 +1500,16 @@ constexpr int kRowsMaxWaves = 16;
 constexpr int kRowsRing = 2;        // rows of loads in flight per wave
 
 // The map `a.map[0]`: tile_start[s] = first row group of segment s (cumulative, each segment's
-// groups padded to a multiple of a.rows_groups), m_tiles = rows per group; a workgroup runs
-// a.rows_groups groups x a.rows_parts K parts, wave w taking part w % rows_parts of group
-// w / rows_parts.
+// groups padded to a multiple of a.rows_groups); a workgroup runs a.rows_groups groups x
+// a.rows_parts K parts, wave w taking part w % rows_parts of group w / rows_parts.
 // (4 waves per SIMD are enough: squeezed for more, the compiler reuses registers that loads
 // in flight still target, which waits for them.)
 template <int DT, int MT, int SP>
 __global__ __launch_bounds__(kRowsMaxWaves * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void gemv_rows_kernel(const GemmArgs a) {
     constexpr int RD = kRowsRing;
-    __shared__ uint32_t s_pair[256];
+    constexpr bool kPrivate = SP == 2;  // one table copy per lane (bank)
+    __shared__ __attribute__((aligned(1024))) uint32_t s_pair[kPrivate ? 256 * 64 : 256];
     __shared__ float s_code2[256];
     __shared__ float s_part[kRowsMaxWaves][MT][64];
     const int np = a.rows_parts;
@@ -1512,10 +1523,11 @@ void gemv_rows_kernel(const GemmArgs a) {
     const int seg = seg_of_tile(a, tm, grp0);
     const int64_t grp = grp0 + wave / np;
     const DevWeight w = a.w[seg];
-    const int64_t row0 = uniform64((grp - tm.tile_start[seg]) * tm.m_tiles);
-    const int64_t left = w.rows - row0;  // <= 0 in a segment's padding groups
-    const int nrows = left <= 0 ? 0 : static_cast<int>(tm.m_tiles < left ? tm.m_tiles : left);
-    const int64_t lrow0 = nrows > 0 ? row0 : 0;  // the rows a padding group loads: row 0
+    const int gs = static_cast<int>(uniform64(tm.tile_start[seg + 1] - tm.tile_start[seg]));
+    const int gi = static_cast<int>(uniform64(grp - tm.tile_start[seg]));
+    // rows gi, gi + gs, .. (none in a padding group, which loads row 0)
+    const int nrows = gi < w.rows ? static_cast<int>((w.rows - gi + gs - 1) / gs) : 0;
+    const int64_t lrow0 = nrows > 0 ? gi : 0;
     const int64_t K = a.K;
     const int khalf = static_cast<int>(K / 2);
     const int lane = threadIdx.x & 63;
@@ -1532,19 +1544,20 @@ void gemv_rows_kernel(const GemmArgs a) {
     const int64_t nblk = (w.rows * w.cols + w.blocksize - 1) >> w.bs_shift;
     const rsrc_t qr = make_rsrc(w.absmax, w.nested ? (nblk + 3) & ~int64_t(3) : 0);
     const int kb = static_cast<int>(K >> w.bs_shift);  // absmax blocks per row
-    const int qbase = static_cast<int>(lrow0) * kb;
 
     // The tables of the workgroup's segment: thread i < 256 (every workgroup has at least 512
-    // threads) writes entry i before the barrier below.  Their loads go first, from every thread
-    // (a branch here would leave them in flight behind the ring loads on some paths, which
-    // makes the loop's wait counts conservative).
+    // threads) writes code2 entry i and pair entry i (one copy), or threads 2e and 2e + 1 the
+    // 64 copies of pair entry e, before the barrier below.  Their loads go first, from every
+    // thread (a branch here would leave them in flight behind the ring loads on some paths,
+    // which makes the loop's wait counts conservative).
     const int i = threadIdx.x & 255;
+    const int e = kPrivate ? (threadIdx.x >> 1) & 255 : i;
     uint32_t hi, lo2, c2;
     {
         const rsrc_t cr = make_rsrc(w.code, 64);
         const rsrc_t c2r = make_rsrc(w.code2, w.nested ? 1024 : 0);
-        hi = bload4(cr, (i >> 4) * 4);
-        lo2 = bload4(cr, (i & 15) * 4);
+        hi = bload4(cr, (e >> 4) * 4);
+        lo2 = bload4(cr, (e & 15) * 4);
         c2 = bload4(c2r, i * 4);
     }
     // LoRA T[m][lane] (dword loads, like the B rows below: no wait here)
@@ -1577,11 +1590,11 @@ void gemv_rows_kernel(const GemmArgs a) {
     const int last = nrows > 0 ? nrows - 1 : 0;
     auto load = [&](int j, int r) {
         const int rr = r < nrows ? r : last;
-        const int64_t row = lrow0 + rr;
+        const int64_t row = lrow0 + static_cast<int64_t>(rr) * gs;
 #pragma unroll
         for (int sl = 0; sl < SP; ++sl) {
             const int byte = 1024 * (slot0 + sl) + 16 * lane;
-            const int b = qbase + rr * kb + lblk[sl];
+            const int b = static_cast<int>(row) * kb + lblk[sl];
             ring[j][sl].p = bload16(wr.packed, static_cast<int>(row * khalf) + byte);
             ring[j][sl].qw = bload4(qr, b & ~3);
             ring[j][sl].s = __builtin_bit_cast(float, bload4(wr.s, (wr.nested ? b >> wr.bs2_shift : b) * 4));
@@ -1599,10 +1612,17 @@ void gemv_rows_kernel(const GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    if (threadIdx.x < 256) {  // write the tables (loaded at the top)
-        s_pair[i] = static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, hi))) |
-                    (static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, lo2))) << 16);
-        s_code2[i] = w.nested ? __builtin_bit_cast(float, c2) : (i == 0 ? 1.0f : 0.0f);
+    if (threadIdx.x < (kPrivate ? 512 : 256)) {  // write the tables (loaded at the top)
+        const uint32_t v = static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, hi))) |
+                           (static_cast<uint32_t>(round16<DT>(__builtin_bit_cast(float, lo2))) << 16);
+        if constexpr (kPrivate) {
+            u32x4_t *dst = reinterpret_cast<u32x4_t *>(s_pair + e * 64 + (threadIdx.x & 1) * 32);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dst[j] = (u32x4_t){v, v, v, v};
+        } else {
+            s_pair[i] = v;
+        }
+        if (threadIdx.x < 256) s_code2[i] = w.nested ? __builtin_bit_cast(float, c2) : (i == 0 ? 1.0f : 0.0f);
     }
     __syncthreads();
 
@@ -1621,7 +1641,15 @@ void gemv_rows_kernel(const GemmArgs a) {
     float res[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) res[m] = 0.0f;
-    const uint32_t *pair = s_pair;
+    const char *pair = reinterpret_cast<const char *>(s_pair);
+    const uint32_t lane4 = static_cast<uint32_t>(lane) * 4;
+    // table entry of byte k of a packed dword: byte address 4 b (one copy), or 256 b + 4 lane
+    // (lane4 in byte 0 and b in byte 1: one v_perm)
+    auto entry = [&](uint32_t pw, int k) -> uint32_t {
+        const uint32_t addr = kPrivate ? vperm(pw, lane4, 0x0C0C0400u | ((4u + k) << 8))
+                                       : ((pw >> (8 * k)) & 0xFFu) * 4;
+        return *reinterpret_cast<const uint32_t *>(pair + addr);
+    };
     const float *code2 = s_code2;
     // Whole rounds of RD rows; the ring slot of a row past the range (a re-read of the last
     // row) is refilled but not computed.
@@ -1637,16 +1665,16 @@ void gemv_rows_kernel(const GemmArgs a) {
 #pragma unroll
             for (int sl = 0; sl < SP; ++sl) {
                 const Slot &sv = ring[j][sl];
-                const int sh = ((qbase + rr * kb + lblk[sl]) & 3) * 8;
+                const int sh = ((static_cast<int>(lrow0 + rr * gs) * kb + lblk[sl]) & 3) * 8;
                 const float sc = absmax_val(w, AbsIn{sv.s, (sv.qw >> sh) & 0xFFu}, code2);
                 const uint32_t pw[4] = {sv.p.x, sv.p.y, sv.p.z, sv.p.w};
                 uint32_t t[16];
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    t[4 * d + 0] = pair[pw[d] & 0xFF];
-                    t[4 * d + 1] = pair[(pw[d] >> 8) & 0xFF];
-                    t[4 * d + 2] = pair[(pw[d] >> 16) & 0xFF];
-                    t[4 * d + 3] = pair[pw[d] >> 24];
+                    t[4 * d + 0] = entry(pw[d], 0);
+                    t[4 * d + 1] = entry(pw[d], 1);
+                    t[4 * d + 2] = entry(pw[d], 2);
+                    t[4 * d + 3] = entry(pw[d], 3);
                 }
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
@@ -1663,8 +1691,8 @@ void gemv_rows_kernel(const GemmArgs a) {
                 }
             }
             {  // LoRA (branch-free: tv is zero without it, and lbw reads zero)
-                const int e = static_cast<int>(lrow0 + rr) * lo.rank + lane;
-                const float bv = to_f32<DT>(static_cast<uint16_t>(lbw[j] >> ((e & 1) * 16)));
+                const int be = static_cast<int>(lrow0 + rr * gs) * lo.rank + lane;
+                const float bv = to_f32<DT>(static_cast<uint16_t>(lbw[j] >> ((be & 1) * 16)));
 #pragma unroll
                 for (int m = 0; m < MT; ++m) acc[m] += lscale * (tv[m] * bv);
             }
@@ -1693,7 +1721,7 @@ void gemv_rows_kernel(const GemmArgs a) {
         }
     }
     if (part == 0 && lane < nrows) {
-        const int64_t col = a.seg_off[seg] + row0 + lane;
+        const int64_t col = a.seg_off[seg] + gi + static_cast<int64_t>(lane) * gs;
         const float bias = a.bias ? to_f32<DT>(a.bias[col]) : 0.0f;
 #pragma unroll
         for (int m = 0; m < MT; ++m)
@@ -2132,9 +2160,9 @@ Plan pinned_plan(int tile, int splits, int64_t big, int64_t small, int64_t steps
 }
 
 // Row-streaming path (M <= 2): K parts of two 1 KB slots (one when a row fits in one slot),
-// workgroups of G row groups x np parts (at most 16 waves), and the fewest rows per group that
-// still fit the launch in one round of workgroups at 4 waves per SIMD (at most 64: one result
-// lane each).  Plan::tiles counts row groups, Plan::waves holds the rows per group, Plan::bp the
+// workgroups of G row groups x np parts (8 waves for one-slot parts, at most 16 otherwise: the
+// kernel's 64-copy table is filled once per CU), and the fewest rows per group that still fit
+// the launch in one round of workgroups at 4 waves per SIMD (at most 64: one result lane each).  Plan::tiles counts row groups, Plan::waves holds the rows per group, Plan::bp the
 // slots per part, Plan::bm the tokens per wave (1 or 2), Plan::splits the parts and
 // Plan::rows_g the groups per workgroup.  From 3 tokens on the decode kernel's MFMA path is
 // faster (its dequant is shared by the tokens).
@@ -2143,7 +2171,7 @@ Plan plan_rows(int64_t m, const nf4_weight *ws, int nw) {
     const int64_t ni = (ws[0].cols / 2 + 1023) / 1024;
     const int sp = ni == 1 ? 1 : 2;
     const int np = static_cast<int>((ni + sp - 1) / sp);
-    const int groups_per_wg = np == 1 ? 8 : kRowsMaxWaves / np;
+    const int groups_per_wg = sp == 1 ? 8 : kRowsMaxWaves / np;
     const int wg_per_cu = kRowsMaxWaves / (np * groups_per_wg) > 1 ? kRowsMaxWaves / (np * groups_per_wg) : 1;
     int64_t rows = 0;
     for (int i = 0; i < nw; ++i) rows += ws[i].rows;
@@ -2386,7 +2414,6 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
         g.splits = 1;
         g.rows_groups = p.rows_g;
         g.rows_parts = p.splits;
-        g.map[0].m_tiles = p.waves;
         g.map[0].tile_start[0] = 0;
         for (int i = 0; i < nw; ++i)
             g.map[0].tile_start[i + 1] =

@@ -361,11 +361,16 @@ def _scaled_codes(p, qs, dtype):
 @pytest.mark.parametrize("m", [1, 2])
 @pytest.mark.parametrize("shapes,bs,nested", [([(384, 256)], 64, True), ([(200, 512)], 128, True),
                                               ([(136, 320)], 64, False),
-                                              ([(256, 512), (64, 512), (64, 512)], 64, True)])
+                                              ([(256, 512), (64, 512), (64, 512)], 64, True),
+                                              ([(200, 3584)], 64, True),
+                                              ([(96, 2560), (40, 2560)], 128, False),
+                                              ([(72, 9472)], 64, True)])
 def test_rows_decode_one_hot_is_exact(cuda, m, shapes, bs, nested, dtype):
     """The row-streaming decode path (M <= 2): token t one-hot at column c_t returns the weight
     column c_t as the GEMV multiplies it - round(fp32(round(code)) * absmax) - bit for bit, over
-    every row of every stacked segment, for columns spread over the reduction."""
+    every row of every stacked segment, for columns spread over the reduction.  K <= 2048 runs
+    the one-copy pair table, longer rows the 64-copy table (two slots per part; K = 9472 in
+    three parts)."""
     from solution import kernels
 
     banner("rows decode one-hot", m, shapes, bs, nested, dtype)
