@@ -200,7 +200,8 @@ int nf4_lora_da(const void *dy, int64_t m, int64_t n, int64_t lddy, const void *
 /* out = scale * U[M, P]^T @ V[M, rank], fp32, reduced over M (the LoRA weight gradients):
  * transpose_out == 0 -> out[P, rank] (dB = s * dY^T @ T, layer.py:1075-1076);
  * transpose_out != 0 -> out[rank, P] (dA = da^T @ xd, layer.py:1080-1081).
- * workspace: nf4_lora_wgrad_workspace() bytes for the split-M partial sums. */
+ * workspace: nf4_lora_wgrad_workspace() bytes for the split-M partial sums (unused when the
+ * one-launch path of nf4_lora_wgrad_multi below applies). */
 int nf4_lora_wgrad(const void *u, int64_t m, int64_t p, int64_t ldu, const void *v, int rank,
                    float scale, float *out, int transpose_out, int dtype,
                    void *workspace, size_t workspace_bytes, void *stream);
@@ -235,8 +236,11 @@ int nf4_lora_ax_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, 
 /* da_j = scale_j * in_j @ B_j for every job (nf4_lora_da per job: layer.py:1074-1078). */
 int nf4_lora_da_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
                       void *stream);
-/* out_j = scale_j * in_j^T @ V_j for every job, one partial and one final launch
- * (nf4_lora_wgrad per job: layer.py:1075-1076, 1080-1081). */
+/* out_j = scale_j * in_j^T @ V_j for every job (nf4_lora_wgrad per job: layer.py:1075-1076,
+ * 1080-1081): one launch over M when every job's rows load as 16-byte pieces (16-byte aligned
+ * `in` with ld % 8 == 0, 16-byte aligned V, rank % 8 == 0) and M <= 4096 or the jobs give 128
+ * or more 32-column tiles (the workspace is then unused); else a partial launch over row chunks
+ * and a fixed-order final launch through the workspace.  Deterministic either way. */
 int nf4_lora_wgrad_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int dtype,
                          void *workspace, size_t workspace_bytes, void *stream);
 size_t nf4_lora_wgrad_multi_workspace(const nf4_lora_job *jobs, int njobs, int64_t m, int rank);

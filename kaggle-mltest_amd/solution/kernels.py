@@ -508,7 +508,8 @@ def lora_ax_job(da: torch.Tensor, a: torch.Tensor, out: torch.Tensor, scale: flo
 
 
 def lora_wgrad_multi(jobs, m: int, rank: int, dtype, stream_tensor: torch.Tensor):
-    """out_j = scale_j * in_j^T @ V_j (fp32) for every job: one partial and one final launch."""
+    """out_j = scale_j * in_j^T @ V_j (fp32) for every job: one launch over M when the rows
+    allow it, else row-chunk partials and a final pass through the workspace."""
     arr, n = _jobs(jobs)
     lib = load()
     nbytes = lib.nf4_lora_wgrad_multi_workspace(arr, n, m, rank)

@@ -325,6 +325,36 @@ def test_lora_multi_matches_single(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,p,ld,rank,transpose", [
+    (2048, 1536, 2048, 16, False),  # one pass over M (aligned rows, ld % 8 == 0, rank % 8 == 0)
+    (300, 100, 104, 8, True),       # ... p not a multiple of the 32-column tile
+    (1, 256, 256, 32, False),
+    (1243, 1000, 1000, 64, True),
+    (37, 72, 72, 24, False),
+    (300, 100, 101, 16, False),     # row chunks + final pass: rows not 16-byte loadable
+    (5000, 64, 64, 16, True),       # ... long M over few workgroups
+    (200, 96, 96, 12, False),       # ... rank not a multiple of 8
+])
+def test_lora_wgrad_paths(cuda, m, p, ld, rank, transpose, dtype):
+    """LoRA weight gradients scale * U^T V (fp32 out, [P, r] or [r, P]) on both kernels (one
+    pass over M, or row chunks with a final fixed-order pass) against fp64 sums of the same
+    16-bit inputs; a second call gives the same bits."""
+    from solution import kernels
+
+    banner("lora wgrad", m, p, ld, rank, transpose, dtype)
+    base = _x(m, ld, 61, cuda, dtype)
+    u = base[:, ld - p:] if (ld - p) % 8 == 0 else base[:, :p]  # rows ld elements apart
+    v = _x(m, rank, 62, cuda, dtype, std=0.1)
+    out = kernels.lora_wgrad(u, v, 0.5, transpose)
+    ref = 0.5 * (u.double().cpu().t() @ v.double().cpu())
+    if transpose:
+        ref = ref.t()
+    assert tuple(out.shape) == tuple(ref.shape)
+    assert_rel(out, ref.float(), max_rel=1e-4, mean_rel=1e-5, what="wgrad")
+    assert torch.equal(out, kernels.lora_wgrad(u, v, 0.5, transpose))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m,inter,k", [(2048, 8960, 1536), (300, 200, 320), (129, 1000, 256)])
 def test_swiglu_epilogue(cuda, m, inter, k, dtype):
     """gate | up with the SwiGLU step in the GEMM epilogue: H = silu(g) u and the gradients
