@@ -2159,19 +2159,22 @@ Plan pinned_plan(int tile, int splits, int64_t big, int64_t small, int64_t steps
     return Plan{tile, b, b, splits, tiles, 0, splits > 1 ? 0 : tiles};
 }
 
-// Row-streaming path (M <= 2): K parts of two 1 KB slots (one when a row fits in one slot),
-// workgroups of G row groups x np parts (8 waves for one-slot parts, at most 16 otherwise: the
-// kernel's 64-copy table is filled once per CU), and the fewest rows per group that still fit
-// the launch in one round of workgroups at 4 waves per SIMD (at most 64: one result lane each).  Plan::tiles counts row groups, Plan::waves holds the rows per group, Plan::bp the
+// Row-streaming path (M <= 2): K parts of one 1 KB slot when a row takes one slot or 3 to
+// kRowsMaxParts slots (the 1.5B down projection, 5 slots: 5 one-slot parts ran 19 % faster than
+// 3 two-slot parts, which left 102 CUs idle and read 27 % past the rows), of two slots
+// otherwise (the 7B rows of 2 slots keep one part and the kernel's 64-copy table); workgroups
+// of G row groups x np parts (8 waves for a single one-slot part, at most 16 otherwise: the
+// 64-copy table is filled once per CU), and the fewest rows per group that still fit the
+// launch in one round of workgroups at 4 waves per SIMD (at most 64: one result lane each).  Plan::tiles counts row groups, Plan::waves holds the rows per group, Plan::bp the
 // slots per part, Plan::bm the tokens per wave (1 or 2), Plan::splits the parts and
 // Plan::rows_g the groups per workgroup.  From 3 tokens on the decode kernel's MFMA path is
 // faster (its dequant is shared by the tokens).
 Plan plan_rows(int64_t m, const nf4_weight *ws, int nw) {
     const int mt = m <= 1 ? 1 : 2;
     const int64_t ni = (ws[0].cols / 2 + 1023) / 1024;
-    const int sp = ni == 1 ? 1 : 2;
+    const int sp = ni == 1 || (ni > 2 && ni <= kRowsMaxParts) ? 1 : 2;
     const int np = static_cast<int>((ni + sp - 1) / sp);
-    const int groups_per_wg = sp == 1 ? 8 : kRowsMaxWaves / np;
+    const int groups_per_wg = sp == 1 && np == 1 ? 8 : kRowsMaxWaves / np;
     const int wg_per_cu = kRowsMaxWaves / (np * groups_per_wg) > 1 ? kRowsMaxWaves / (np * groups_per_wg) : 1;
     int64_t rows = 0;
     for (int i = 0; i < nw; ++i) rows += ws[i].rows;
