@@ -9,10 +9,10 @@ layer reads fixed input buffers, so a step is exactly the projection work of the
 
 Every launch goes through the C ABI with argument arrays built once, on torch's current
 stream, in the order the reference runs them:
-  forward, per layer:  t_q = X A_q^T and t_v = X A_v^T (one launch); q|k|v (+bias, +LoRA);
-                       o; gate|up; down
+  forward, per layer:  t_q = X A_q^T and t_v = X A_v^T (one launch, kept per layer for the
+                       backward); q|k|v (+bias, +LoRA); o; gate|up; down
   backward, reversed:  dX down; dX gate|up; dX o; da_q, da_v (one launch); dB_q, dB_v, dA_q,
-                       dA_v (one partial + one final launch); dX q|k|v (+LoRA)
+                       dA_v (one launch); dX q|k|v (+LoRA)
 """
 
 from __future__ import annotations
@@ -84,7 +84,7 @@ class ProjectionStack:
         self.dy_qkv, self.dy_o = rnd((mt, self.n_qkv), 2, 1e-3), rnd((mt, h), 21, 1e-3)
         self.dy_gu, self.dy_d = rnd((mt, 2 * i), 22, 1e-3), rnd((mt, h), 23, 1e-3)
         e = lambda *s: torch.empty(s, dtype=dtype, device=self.dev)  # noqa: E731
-        self.t_q, self.t_v, self.da_q, self.da_v = e(mt, rank), e(mt, rank), e(mt, rank), e(mt, rank)
+        self.da_q, self.da_v = e(mt, rank), e(mt, rank)
         self.y_qkv, self.y_o, self.y_gu, self.y_d = e(mt, self.n_qkv), e(mt, h), e(mt, 2 * i), e(mt, h)
         self.dx_d, self.dx_gu, self.dx_o, self.dx_qkv = e(mt, i), e(mt, h), e(mt, h), e(mt, h)
 
@@ -107,20 +107,21 @@ class ProjectionStack:
             f = lambda *s: torch.empty(s, dtype=torch.float32, device=self.dev)  # noqa: E731
             L["gb_q"], L["gb_v"], L["ga_q"], L["ga_v"] = f(h, rank), f(kv, rank), f(rank, h), f(rank, h)
             P, Lo = (lambda t: t.data_ptr()), _lib.NF4Lora
-            L["fwd_loras"] = (Lo * 2)(Lo(0, rank, self.scale, P(self.t_q), P(L["b_q"]), None, None),
-                                      Lo(2, rank, self.scale, P(self.t_v), P(L["b_v"]), None, None))
+            L["t_q"], L["t_v"] = e(mt, rank), e(mt, rank)  # t = X A^T, read again by dB
+            L["fwd_loras"] = (Lo * 2)(Lo(0, rank, self.scale, P(L["t_q"]), P(L["b_q"]), None, None),
+                                      Lo(2, rank, self.scale, P(L["t_v"]), P(L["b_v"]), None, None))
             L["dx_loras"] = (Lo * 2)(Lo(0, rank, self.scale, None, None, P(L["a_q"]), P(self.da_q)),
                                      Lo(2, rank, self.scale, None, None, P(L["a_v"]), P(self.da_v)))
             # the side products of both adapters, one launch each (nf4_lora_job arrays)
             J, es = _lib.NF4LoraJob, self.dy_qkv.element_size()
             dq, dv = P(self.dy_qkv), P(self.dy_qkv) + (h + kv) * es
             nq = self.n_qkv
-            L["xa_jobs"] = (J * 2)(J(P(self.x), h, h, P(L["a_q"]), P(self.t_q), 1.0, 0),
-                                   J(P(self.x), h, h, P(L["a_v"]), P(self.t_v), 1.0, 0))
+            L["xa_jobs"] = (J * 2)(J(P(self.x), h, h, P(L["a_q"]), P(L["t_q"]), 1.0, 0),
+                                   J(P(self.x), h, h, P(L["a_v"]), P(L["t_v"]), 1.0, 0))
             L["da_jobs"] = (J * 2)(J(dq, nq, h, P(L["b_q"]), P(self.da_q), self.scale, 0),
                                    J(dv, nq, kv, P(L["b_v"]), P(self.da_v), self.scale, 0))
-            L["wg_jobs"] = (J * 4)(J(dq, nq, h, P(self.t_q), P(L["gb_q"]), self.scale, 0),
-                                   J(dv, nq, kv, P(self.t_v), P(L["gb_v"]), self.scale, 0),
+            L["wg_jobs"] = (J * 4)(J(dq, nq, h, P(L["t_q"]), P(L["gb_q"]), self.scale, 0),
+                                   J(dv, nq, kv, P(L["t_v"]), P(L["gb_v"]), self.scale, 0),
                                    J(P(self.x), h, h, P(self.da_q), P(L["ga_q"]), 1.0, 1),
                                    J(P(self.x), h, h, P(self.da_v), P(L["ga_v"]), 1.0, 1))
             self.per_layer.append(L)

@@ -70,3 +70,33 @@ def test_stack_token_count_changes(cuda):
         assert_rel(st.y_d[:m], o.linear_fwd(st.act[:m], W["down"]), what=f"down M={m}")
     with pytest.raises(ValueError):
         st.set_tokens([0, 300])
+
+
+def test_stack_full_step_lora_grads(cuda):
+    """A whole step (every layer's forward, then every layer's backward): each layer's dA / dB
+    against the oracle from that layer's own t (kept per layer), and the q|k|v input gradient
+    of the last layer run (layer 0)."""
+    from solution.stack import ProjectionStack, Qwen2Shape
+
+    shape = Qwen2Shape(hidden=256, inter=640, kv=64)
+    banner("stack full step, 3 layers")
+    st = ProjectionStack.synthetic(shape, 3, 512, torch.float16, cuda, seed_base=29, rank=16,
+                                   alpha=32)
+    m = st.set_tokens([0, 100, 300])
+    st.step()
+    torch.cuda.synchronize()
+    s = st.scale
+    x, dy_qkv = st.x[:m], st.dy_qkv[:m]
+    for li in range(3):
+        L = st.per_layer[li]
+        ga_q, gb_q = o.lora_grads(dy_qkv[:, :256], x, L["a_q"], L["b_q"], s)
+        ga_v, gb_v = o.lora_grads(dy_qkv[:, 320:], x, L["a_v"], L["b_v"], s)
+        assert_rel(L["gb_q"], gb_q, what=f"L{li} dB_q")
+        assert_rel(L["ga_q"], ga_q, what=f"L{li} dA_q")
+        assert_rel(L["gb_v"], gb_v, what=f"L{li} dB_v")
+        assert_rel(L["ga_v"], ga_v, what=f"L{li} dA_v")
+    W = {n: oracle_w16(*st.layers[0][n]) for n in st.layers[0]}
+    wqkv = torch.cat([W["q"], W["k"], W["v"]])
+    L0 = st.per_layer[0]
+    lor = [(0, 256, x, L0["a_q"], L0["b_q"], s), (320, 64, x, L0["a_v"], L0["b_v"], s)]
+    assert_rel(st.dx_qkv[:m], o.linear_dx(dy_qkv, wqkv, lor), what="L0 dx qkv")
