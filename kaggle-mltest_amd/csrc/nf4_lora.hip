@@ -55,6 +55,17 @@ __device__ __forceinline__ u32x4_t frag8(const uint16_t *src, int64_t stride, in
 
 constexpr int kMaxRank = 64;
 
+// ds_read_b64_tr_b16: in each 16-lane group lane q points at 4 consecutive 16-bit columns of
+// row r0 + q / 4 of a row-major LDS tile and receives column q of rows r0 .. r0 + 3.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+__device__ __forceinline__ uint2 tr_read(const uint8_t *s, int off) {
+    const v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16_t *)((__attribute__((address_space(3))) uint8_t *)s + off));
+    return __builtin_bit_cast(uint2, v);
+}
+
 // One LoRA side product of a launch (the C ABI's nf4_lora_job plus host-computed layout).
 struct Job {
     const uint16_t *in;   // rowdot: act rows; wgrad: U rows (already at their column offset)
@@ -64,7 +75,8 @@ struct Job {
     void *out;
     float scale;
     int transpose;        // wgrad: out is [rank, P]
-    int vec;              // rowdot: bit 0 act rows 16-byte loadable, bit 1 A rows; wgrad: U rows
+    int vec;              // rowdot: bit 0 act rows 16-byte loadable, bit 1 A rows, bit 2 B rows;
+                          // wgrad: U rows
     int64_t part_off;     // wgrad: float offset of this job's partials in the workspace
     int64_t out_start;    // wgrad: first output element of this job in the final grid
     int64_t tile0;        // one-pass wgrad: first workgroup of this job
@@ -80,14 +92,20 @@ struct Jobs {
 //   W(j, k) = w[k * rank + j] (B_LAYOUT true:  LoRA B [N, rank], for da = s dY B).
 // A workgroup owns 16 rows m; its 16 waves split the reduction (short per-wave ranges keep
 // many loads in flight, also when M is a handful of tokens) and add their 16 x 16 partial tiles
-// through LDS in a fixed order.  MFMA A operand = W (rows j), B operand = act (cols m).
+// through LDS in a fixed order.  MFMA A operand = W (rows j), B operand = act (cols m).  In the
+// B layout a 32-deep slice of B (32 rows of 16 ranks, 16-byte loads) goes through the wave's
+// own LDS tile and comes back transposed (tr_read) as the A fragments, in place of 8 strided
+// 2-byte loads per fragment.
 constexpr int kRowdotWaves = 16;
 
-template <int DT, bool B_LAYOUT>
+template <int DT, bool B_LAYOUT, bool BV = false>
 __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jobs, int64_t m,
                                                                      int rank) {
+    static_assert(!BV || B_LAYOUT, "B rows through LDS in the B layout only");
     __shared__ float4_t red[kRowdotWaves][64];
+    __shared__ __attribute__((aligned(16))) uint8_t sB[BV ? kRowdotWaves : 1][32 * 32];
     const Job &jb = jobs.j[blockIdx.y];
+    const rsrc_t brs = make_rsrc(jb.w, BV ? jb.cols * rank * 2 : 0);  // BV: every job's B rows 16-byte loadable
     const uint16_t *act = jb.in, *w = jb.w;
     const int64_t k = jb.cols, ld = jb.ld;
     uint16_t *out = static_cast<uint16_t *>(jb.out);
@@ -103,22 +121,36 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jo
         float4_t acc = {0.f, 0.f, 0.f, 0.f};
         const int j = j0 + col;
         // U 32-deep slices per group: all their loads are issued before the first MFMA, so a
-        // wave waits for one memory latency per group, not per slice (the strided B-layout
-        // gathers hold 8 scalar loads per fragment: two slices fit the registers)
-        constexpr int kRowdotUnroll = B_LAYOUT ? 2 : 8;
+        // wave waits for one memory latency per group, not per slice
+        constexpr int kRowdotUnroll = B_LAYOUT && !BV ? 2 : B_LAYOUT ? 4 : 8;
         for (int64_t k0 = kb; k0 < ke; k0 += 32 * kRowdotUnroll) {
-            u32x4_t fa[kRowdotUnroll], fb[kRowdotUnroll];
+            u32x4_t fa[kRowdotUnroll], fb[kRowdotUnroll], rb[BV ? kRowdotUnroll : 1];
 #pragma unroll
             for (int u = 0; u < kRowdotUnroll; ++u) {
                 const int64_t kk = k0 + 32 * u + kq;
                 const int lim = ke - kk < 8 ? static_cast<int>(ke - kk) : 8;
                 fa[u] = (u32x4_t){0u, 0u, 0u, 0u};
                 fb[u] = (u32x4_t){0u, 0u, 0u, 0u};
-                if (lim > 0) {
-                    if (j < rank)
-                        fa[u] = B_LAYOUT ? frag8(w + kk * rank + j, rank, lim, false)
-                                         : frag8(w + j * k + kk, 1, lim, (jb.vec & 2) != 0);
-                    if (row < m) fb[u] = frag8(act + row * ld + kk, 1, lim, (jb.vec & 1) != 0);
+                if constexpr (BV) {
+                    // rows k0 + 32 u + lane / 2 of B, ranks j0 + 8 (lane % 2) ..: rows past K
+                    // read as zero, rows past the wave's range meet zero activations, ranks
+                    // past the rank reach outputs that are not stored
+                    rb[u] = bload16(brs, static_cast<int>(((k0 + 32 * u + (lane >> 1)) * rank +
+                                                           j0 + (lane & 1) * 8) * 2));
+                } else if (lim > 0 && j < rank) {
+                    fa[u] = B_LAYOUT ? frag8(w + kk * rank + j, rank, lim, false)
+                                     : frag8(w + j * k + kk, 1, lim, (jb.vec & 2) != 0);
+                }
+                if (lim > 0 && row < m) fb[u] = frag8(act + row * ld + kk, 1, lim, (jb.vec & 1) != 0);
+            }
+            if constexpr (BV) {
+                uint8_t *sb = sB[wave];
+                const int r0 = 8 * (lane >> 4) + ((lane & 15) >> 2), c4 = (lane & 3) * 8;
+#pragma unroll
+                for (int u = 0; u < kRowdotUnroll; ++u) {
+                    *reinterpret_cast<u32x4_t *>(sb + (lane >> 1) * 32 + (lane & 1) * 16) = rb[u];
+                    const uint2 lo = tr_read(sb, r0 * 32 + c4), hi = tr_read(sb, (r0 + 4) * 32 + c4);
+                    fa[u] = (u32x4_t){lo.x, lo.y, hi.x, hi.y};
                 }
             }
 #pragma unroll
@@ -340,15 +372,6 @@ constexpr int kWgCols = 32;
 constexpr int kWgRing = 4;
 constexpr int kWgWaves = 8;
 constexpr int64_t kWgPastRows = 32 * kWgWaves * 3 * kWgRing;  // rows the ring may load past M
-
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
-
-__device__ __forceinline__ uint2 tr_read(const uint8_t *s, int off) {
-    const v4i16_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (lds_v4i16_t *)((__attribute__((address_space(3))) uint8_t *)s + off));
-    return __builtin_bit_cast(uint2, v);
-}
 
 template <int DT>
 __global__ __launch_bounds__(kWgWaves * 64) void wgrad_direct_kernel(const Jobs jobs, int64_t m,
@@ -600,7 +623,9 @@ int rowdot_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int d
     for (int i = 0; i < njobs; ++i) {
         Job &j = J.j[i];
         j.vec = (j.ld % 8 == 0 && aligned(j.in, 16) ? 1 : 0) |
-                (!B_LAYOUT && j.cols % 8 == 0 && aligned(j.w, 16) ? 2 : 0);
+                (!B_LAYOUT && j.cols % 8 == 0 && aligned(j.w, 16) ? 2 : 0) |
+                (B_LAYOUT && rank % 8 == 0 && aligned(j.w, 16) &&
+                 (j.cols + 64) * rank * 2 < (int64_t(1) << 31) ? 4 : 0);
     }
     auto s = static_cast<hipStream_t>(stream);
     bool vec = true;
@@ -624,7 +649,16 @@ int rowdot_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int d
         return status_of(hipGetLastError());
     }
     const dim3 grid(static_cast<unsigned>((m + 15) / 16), static_cast<unsigned>(njobs));
-    if (dtype == NF4_BF16)
+    bool bv = B_LAYOUT;
+    for (int i = 0; i < njobs; ++i) bv = bv && (J.j[i].vec & 4) != 0;
+    if (bv) {
+        if (dtype == NF4_BF16)
+            hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, true, true>), grid, dim3(kRowdotWaves * 64),
+                               0, s, J, m, rank);
+        else
+            hipLaunchKernelGGL((rowdot_kernel<NF4_F16, true, true>), grid, dim3(kRowdotWaves * 64),
+                               0, s, J, m, rank);
+    } else if (dtype == NF4_BF16)
         hipLaunchKernelGGL((rowdot_kernel<NF4_BF16, B_LAYOUT>), grid, dim3(kRowdotWaves * 64), 0,
                            s, J, m, rank);
     else
