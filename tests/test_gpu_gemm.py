@@ -325,6 +325,28 @@ def test_lora_multi_matches_single(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,n,rank,offset", [(300, 1000, 8, 0), (2048, 1536, 16, 0),
+                                             (77, 256, 24, 0), (129, 640, 64, 0),
+                                             (300, 1000, 12, 0), (200, 512, 16, 1)])
+def test_lora_da_xa_ranks(cuda, m, n, rank, offset, dtype):
+    """da = s dY B and t = X A^T at ranks 8..64 (B rows 16-byte loadable through the LDS
+    transpose, or strided gathers: rank 12, or B starting one element in) against fp64 sums of
+    the same 16-bit inputs."""
+    from solution import kernels
+
+    banner("lora da/xa ranks", m, n, rank, offset, dtype)
+    dy = _x(m, n, 71, cuda, dtype, std=0.1)
+    bbuf = _x(n * rank + offset, 1, 72, cuda, dtype, std=0.1).view(-1)
+    b = bbuf[offset:].view(n, rank)
+    da = kernels.lora_da(dy, b, 1.5)
+    ref = 1.5 * (dy.double().cpu() @ b.double().cpu())
+    assert_rel(da, ref.float(), what="da")
+    a = _x(rank, n, 73, cuda, dtype, std=0.1)
+    t = kernels.lora_xa(dy, a)
+    assert_rel(t, (dy.double().cpu() @ a.double().cpu().t()).float(), what="xa")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m,p,ld,rank,transpose", [
     (2048, 1536, 2048, 16, False),  # one pass over M (aligned rows, ld % 8 == 0, rank % 8 == 0)
     (300, 100, 104, 8, True),       # ... p not a multiple of the 32-column tile
