@@ -981,10 +981,15 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
     // this group's steps: s0 + g + KG v for v < nv (the same nv in every group)
     const int64_t nv = (s1 - s0 + KG - 1) / KG;
 
-    for (int i = threadIdx.x; i < 256; i += KG * NT) {
-        s_code2[0][i] = code2_entry(a.w[seg], i);
-        if constexpr (PAIR) s_code2[1][i] = code2_entry(a.w[1], i);
-    }
+    // code2 table entry threadIdx.x (every workgroup has at least 256 threads): loaded here,
+    // written to LDS after the first two steps' loads and the LoRA slab's are issued, so that
+    // their latency is not behind this load's
+    // (buffer loads with no branch: threads past entry 255, and weights without nested
+    // absmax, read zero)
+    static_assert(KG * NT >= 256, "one code2 entry per thread");
+    const int ci = static_cast<int>(threadIdx.x);
+    const uint32_t c2a = bload4(make_rsrc(a.w[seg].code2, a.w[seg].nested ? 1024 : 0), ci * 4);
+    const uint32_t c2b = PAIR ? bload4(make_rsrc(a.w[1].code2, a.w[1].nested ? 1024 : 0), ci * 4) : 0u;
     const float *code2 = s_code2[PAIR ? wseg : 0];
     float code_r[16];
     load_code_sgpr(w.code, code_r);
@@ -1059,6 +1064,11 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
             for (int j = 0; j < TM; ++j) acc[i][j] *= lo.scale;
     }
 
+    if (ci < 256) {
+        const float one = ci == 0 ? 1.0f : 0.0f;  // the table of a weight without nested absmax
+        s_code2[0][ci] = a.w[seg].nested ? __builtin_bit_cast(float, c2a) : one;
+        if constexpr (PAIR) s_code2[1][ci] = a.w[1].nested ? __builtin_bit_cast(float, c2b) : one;
+    }
     __syncthreads();  // tables
     uint8_t *sW[2] = {sT[g][0], sT[g][1]};
     uint8_t *sA[2] = {sT[g][0] + BP * ROWB, sT[g][1] + BP * ROWB};
