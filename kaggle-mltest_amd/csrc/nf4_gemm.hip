@@ -257,7 +257,8 @@ __device__ __forceinline__ ActAddr act_addr(int64_t ld) {
     return r;
 }
 
-// BM rows x 64 columns of act[m][col0 ..] staged through registers: load() issues the global
+// BM rows x 64 columns of act[m][col0 ..] staged through registers (the dX kernels' dY tile,
+// whose partial steps are masked in registers; the forward tile goes by LDS DMA): load() issues the global
 // loads of a step (16 bytes per chunk, 8 consecutive threads per 128-byte row), store() writes
 // them to an LDS tile after the current step's MFMAs, so the wait for the loads lands there.
 // Rows >= M read as zero.
@@ -1004,30 +1005,58 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = (float16_t){};
 
-    // Two register stages (steps v+1 and v+2 in flight) and two LDS stages (v and v+1), in the
-    // group's step numbering v.  Step v computes from LDS stage v & 1 while the other LDS stage
-    // receives step v+1 from register stage (v + 1) & 1, a quarter per MFMA k-substep; the
-    // register stage of v has been consumed, so it takes the global loads of v+2.  The loop
+    // Two LDS stages (steps v and v+1, in the group's step numbering v) and two weight register
+    // stages.  Step v computes from LDS stage v & 1 while the other LDS stage receives step v+1:
+    // its weights from register stage (v + 1) & 1, dequantized a quarter per MFMA k-substep, and
+    // its activations straight from global memory by gfx950's 16-byte LDS DMA
+    // (buffer_load_dwordx4 ... lds: lane i of the wave writes M0 + 16 i), issued after the
+    // first quarter, when the weight registers of v+1 have been consumed; the global loads of
+    // the weights of v+2 go out with it.  Wave w of a group fills the 8-row blocks CHA w ..
+    // CHA w + CHA - 1 of the activation tile, lane i's source chunk chosen so that the block
+    // lands in swz()'s layout (row r, position q holds chunk q ^ ((r >> 1) & 7)).  The loop
     // body has no branches: prefetches past the range are issued anyway (in bounds of the
-    // operands or zero from the buffer range check, never consumed), so the compiler's wait
-    // counts only wait for the loads a store needs, never for the prefetch just issued.  An odd
-    // last step runs after the loop.  A group's step past the workgroup's range (KG > 1 only)
-    // reads its activations from an empty resource: zeros, so it adds nothing.  The loads of the
-    // first two steps are issued before the LoRA slab and the table barrier, so that their
-    // latency overlaps the slab's loads.
+    // operands or zero from the buffer range check, never consumed).  An odd last step runs
+    // after the loop.  Rows past M, and a group's step past the workgroup's range (KG > 1 only,
+    // an empty resource), read zeros.  The first two steps' loads are issued before the LoRA
+    // slab and the table barrier, so that their latency overlaps the slab's loads.
     FwdWeight<DT, BP> wt[2] = {};
-    ActTile<BM, NT> at[2] = {};
     const WeightRsrc wr = weight_rsrc(w);
     const rsrc_t ar = act_rsrc<BM>(a, m0);
     const rsrc_t ar0 = make_rsrc(a.act, 0);
-    const ActAddr aa = act_addr<NT>(a.ld_act);
     const WAddr wa = fwd_waddr<BP>(wr, p0 - (wseg == 1 ? PH : 0), K);
-    auto stage = [&](int b, int64_t v) {
+    constexpr int CHA = BM * 8 / NT;
+    static_assert(CHA >= 1 && BM * 8 % NT == 0, "activation rows split evenly over the waves");
+    int adoff[CHA];
+#pragma unroll
+    for (int j = 0; j < CHA; ++j) {
+        const int row = (wave * CHA + j) * 8 + (lane >> 3);
+        adoff[j] = row * static_cast<int>(a.ld_act) * 2 + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
+    }
+    const uint32_t lds_a =  // this wave's activation rows in the group's LDS stage 0
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t *)lds)) +
+        (g * NS * (BP + BM) + BP + wave * CHA * 8) * ROWB;
+    // The DMA as inline assembly: the compiler does not count these loads, so none of its own
+    // waits (for the weight registers) also waits for them; wait_dma() waits for them instead.
+    auto dma_a = [&](int b, int64_t v) {  // activations of step v into LDS stage b
         const int64_t st = s0 + g + KG * v;
-        at[b].load(KG > 1 && st >= s1 ? ar0 : ar, aa, static_cast<int>(st) * (BR * 2));
-        wt[b].load(wr, wa, st);
+        const rsrc_t rs = KG > 1 && st >= s1 ? ar0 : ar;
+        const int kb = static_cast<int>(st) * (BR * 2);
+        const uint32_t base = __builtin_amdgcn_readfirstlane(lds_a + b * (BP + BM) * ROWB);
+#pragma unroll
+        for (int j = 0; j < CHA; ++j) {
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                         :
+                         : "s"(base + j * 8 * ROWB), "v"(adoff[j]), "s"(rs), "s"(kb)
+                         : "memory", "m0");
+        }
     };
+    // Every DMA is followed by exactly the 3 global loads of one weight register stage (packed
+    // bytes, absmax code, absmax scale) and by nothing else before this wait, and loads complete
+    // in order: vmcnt(3) has this wave's DMA in LDS.
+    auto wait_dma = [] { asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); };
+    auto stage = [&](int b, int64_t v) { wt[b].load(wr, wa, s0 + g + KG * v); };
     if (nv > 0) {
+        dma_a(0, 0);
         stage(0, 0);
         stage(1, 1);
     }
@@ -1073,24 +1102,27 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
     uint8_t *sW[2] = {sT[g][0], sT[g][1]};
     uint8_t *sA[2] = {sT[g][0] + BP * ROWB, sT[g][1] + BP * ROWB};
     if (nv > 0) {
-        at[0].store(sA[0]);
         {
             const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
 #pragma unroll
             for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
         }
+        wait_dma();
         __syncthreads();
         int64_t v = 0;
         for (; v + 1 < nv; v += 2) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                stage(b, v + b + 2);
                 const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
                 mma_step_interleaved<DT, TP, TM, PH>(
                     acc, sW[b], sA[b], prow0, wm * (BM / WM), [&](int ks) {
-                        at[b ^ 1].store_part(sA[b ^ 1], ks);
                         wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                        if (ks == 0) {
+                            dma_a(b ^ 1, v + b + 1);
+                            stage(b, v + b + 2);
+                        }
                     });
+                wait_dma();
                 __syncthreads();
             }
         }
