@@ -1842,19 +1842,32 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
     uint8_t *sW[2] = {sT[g][0], sT[g][1]};
     uint8_t *sA[2] = {sT[g][0] + BP * ROWB, sT[g][1] + BP * ROWB};
     DxWeight<DT, BP> wt[2] = {};
-    ActTile<BM, NT> at[2] = {};
-    int vld[2] = {BR, BR};  // valid dY columns of each register stage
     const rsrc_t ar = act_rsrc<BM>(a, m0);
     const rsrc_t ar0 = make_rsrc(a.act, 0);
-    const ActAddr aa = act_addr<NT>(a.ld_act);
+    // the dY tile by LDS DMA, as the forward kernel's activation tile
+    constexpr int CHA = BM * 8 / NT;
+    static_assert(CHA >= 1 && BM * 8 % NT == 0, "dY rows split evenly over the waves");
+    int adoff[CHA];
+#pragma unroll
+    for (int j = 0; j < CHA; ++j) {
+        const int row = (wave * CHA + j) * 8 + (lane >> 3);
+        adoff[j] = row * static_cast<int>(a.ld_act) * 2 + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
+    }
+    const uint32_t lds_a =  // this wave's dY rows in the group's LDS stage 0
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t *)lds)) +
+        (g * NS * (BP + BM) + BP + wave * CHA * 8) * ROWB;
+    // every DMA is followed by exactly one weight register stage's 3 loads before this wait
+    auto wait_dma = [] { asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); };
     __syncthreads();  // tables
     // The reduction range [s0, s1) walks the stacked segments in order; each segment runs the
-    // forward kernel's pipeline (two register stages, two LDS stages, next tile's staging
-    // interleaved with the MFMAs, no branches in the loop body, odd step after the loop) over
-    // the group's steps b0 + g + KG v of the segment, with the segment's descriptor held in
-    // registers.  A segment's partial last step (rows % 64 != 0) has its dY columns past the
-    // segment zeroed in registers before they reach LDS; rows past the weight dequantize
-    // from zero bytes and meet those zeros.
+    // forward kernel's pipeline (two weight register stages, two LDS stages, the next step's
+    // dequant interleaved with the MFMAs and its dY tile sent by LDS DMA after the first
+    // k-substep, no branches in the loop body, odd step after the loop) over the group's steps
+    // b0 + g + KG v of the segment, with the segment's descriptor held in registers.  A
+    // segment's partial last step (rows % 64 != 0) has its dY columns past the segment zeroed
+    // in LDS once its DMA has landed (a branch and a barrier that the whole workgroup takes
+    // when any group's step is such a step); rows past the weight dequantize from zero bytes
+    // and meet those zeros.
     for (int seg = seg_of_step(a, s0); seg < a.nseg && a.step_start[seg] < s1; ++seg) {
         const int64_t first = a.step_start[seg];
         const int64_t b0 = first > s0 ? first : s0;
@@ -1868,37 +1881,78 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
         const float *code2 = s_code2[seg];
         float code_r[16];
         load_code_sgpr(w.code, code_r);
-        auto stage = [&](int b, int64_t v) {
+        auto dma_a = [&](int b, int64_t v) {  // dY columns of step v into LDS stage b
             const int64_t st = b0 + g + KG * v;
-            const int64_t n0 = (st - first) * BR;
-            at[b].load(KG > 1 && st >= e0 ? ar0 : ar, aa, static_cast<int>((col_base + n0) * 2));
-            wt[b].load(wr, wa, n0, K);
-            vld[b] = w.rows - n0 < BR ? static_cast<int>(w.rows - n0) : BR;
+            const rsrc_t rs = KG > 1 && st >= e0 ? ar0 : ar;
+            const int kb = static_cast<int>((col_base + (st - first) * BR) * 2);
+            const uint32_t base = __builtin_amdgcn_readfirstlane(lds_a + b * (BP + BM) * ROWB);
+#pragma unroll
+            for (int j = 0; j < CHA; ++j) {
+                asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                             :
+                             : "s"(base + j * 8 * ROWB), "v"(adoff[j]), "s"(rs), "s"(kb)
+                             : "memory", "m0");
+            }
+        };
+        auto stage = [&](int b, int64_t v) { wt[b].load(wr, wa, (b0 + g + KG * v - first) * BR, K); };
+        // After the DMA of step v into stage b has landed and the barrier: zero its columns past
+        // the segment if step v is the segment's partial last step in any group.
+        auto mask_lds = [&](int b, int64_t v) {
+            bool any = false;
+            int mine = BR;
+#pragma unroll
+            for (int gg = 0; gg < KG; ++gg) {
+                const int64_t st = b0 + gg + KG * v;
+                const int64_t left = w.rows - (st - first) * BR;
+                const bool part = v < nv && st < e0 && left < BR;
+                any = any || part;
+                if (gg == g && part) mine = static_cast<int>(left);
+            }
+            if (!any) return;
+            if (mine < BR) {
+                for (int idx = threadIdx.x % NT; idx < BM * 8; idx += NT) {
+                    const int row = idx >> 3, c = idx & 7;
+                    const int k = mine - c * 8;  // valid elements of chunk c
+                    if (k >= 8) continue;
+                    u32x4_t *q = reinterpret_cast<u32x4_t *>(sA[b] + swz(row, c));
+                    uint32_t mk[4];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+                        mk[d] = ((2 * d < k) ? 0x0000ffffu : 0u) | ((2 * d + 1 < k) ? 0xffff0000u : 0u);
+                    const u32x4_t x = *q;
+                    *q = (u32x4_t){x.x & mk[0], x.y & mk[1], x.z & mk[2], x.w & mk[3]};
+                }
+            }
+            __syncthreads();
         };
         __syncthreads();  // the previous segment's last MFMAs have read the LDS stages
+        dma_a(0, 0);
         stage(0, 0);
         stage(1, 1);
-        if (vld[0] < BR) at[0].mask(vld[0]);
-        at[0].store(sA[0]);
         {
             const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
 #pragma unroll
             for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
         }
+        wait_dma();
         __syncthreads();
+        mask_lds(0, 0);
         int64_t v = 0;
         for (; v + 1 < nv; v += 2) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                stage(b, v + b + 2);
                 const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
                 mma_step_dx<DT, BP, TP, TM>(
                     acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
-                        if (ks == 0 && vld[b ^ 1] < BR) at[b ^ 1].mask(vld[b ^ 1]);
-                        at[b ^ 1].store_part(sA[b ^ 1], ks);
                         wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                        if (ks == 0) {
+                            dma_a(b ^ 1, v + b + 1);
+                            stage(b, v + b + 2);
+                        }
                     });
+                wait_dma();
                 __syncthreads();
+                mask_lds(b ^ 1, v + b + 1);
             }
         }
         if (v < nv)
