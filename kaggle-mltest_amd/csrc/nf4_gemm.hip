@@ -1037,6 +1037,8 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
         (g * NS * (BP + BM) + BP + wave * CHA * 8) * ROWB;
     // The DMA as inline assembly: the compiler does not count these loads, so none of its own
     // waits (for the weight registers) also waits for them; wait_dma() waits for them instead.
+    // M0 is declared clobbered (hipcc notes that it is a reserved register): nothing else in
+    // these kernels uses M0, so no value of the compiler's lives in it across the statement.
     auto dma_a = [&](int b, int64_t v) {  // activations of step v into LDS stage b
         const int64_t st = s0 + g + KG * v;
         const rsrc_t rs = KG > 1 && st >= s1 ? ar0 : ar;
