@@ -69,7 +69,7 @@ def parse():
                     help="skip the int8 MLP input-gradient leg (the reference's T4 backward)")
     ap.add_argument("--no-norm-rope", action="store_true",
                     help="skip the RMSNorm / RoPE neighbours of the projection")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times: the "
                          "known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -423,25 +423,27 @@ def dequant_leg(dtype, dev, reps=5):
 
     lib = _lib.load()
     dt = _lib.DTYPE_CODE[dtype]
-    base = {}
-    for i, (name, n, k) in enumerate(LAYER):
-        g = torch.Generator(device=dev).manual_seed(1000 + i)
-        packed, qs = quantize_4bit(torch.randn(n, k, generator=g, device=dev) * 0.02)
-        base[name] = (packed.view(-1), qs)
+    shapes = {name: (n, k) for name, n, k in LAYER}
     groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
     grouped, batched, keep = [], [], []
     total_bytes = write_bytes = 0
     for layer in range(28):
+        # every layer's weights quantized on their own (seeds 1000 + 7 layer + i): packed bytes,
+        # absmax codes and absmax2 scales all distinct, the whole stack the working set
+        base = {}
+        for i, (name, n, k) in enumerate(LAYER):
+            g = torch.Generator(device=dev).manual_seed(1000 + 7 * layer + i)
+            packed, qs = quantize_4bit(torch.randn(n, k, generator=g, device=dev) * 0.02)
+            base[name] = (packed.view(-1), qs)
+            keep += [packed, qs]
         layer_descs, layer_outs = [], []
         for names in groups:
             descs, rows = [], 0
             for nm in names:
                 p, qs = base[nm]
-                p2 = p.clone()  # a distinct copy per layer: the working set is the whole stack
-                keep.append(p2)
-                descs.append(weight_desc(p2, qs))
+                descs.append(weight_desc(p, qs))
                 rows += int(qs.shape[0])
-            cols = int(base[names[0]][1].shape[1])
+            cols = shapes[names[0]][1]
             out = torch.empty((rows, cols), dtype=dtype, device=dev)
             keep.append(out)
             arr = (_lib.NF4Weight * len(descs))(*descs)
@@ -506,7 +508,8 @@ def dequant_leg(dtype, dev, reps=5):
             "bytes_per_pass": total_bytes, "read_bytes": total_bytes - write_bytes,
             "write_bytes": write_bytes, "us_per_pass": round(table_ms * 1e3, 1),
             "launches_per_pass": 1, "workgroups": int(blocks.value),
-            "working_set": "28-layer Qwen2.5-1.5B stack (196 weights)",
+            "working_set": "28-layer Qwen2.5-1.5B stack (196 weights, each quantized on its own: "
+                           "distinct packed bytes, absmax codes and absmax2 scales)",
             "timing": "one nf4_dequant_table launch over all 196 weights, HIP events, mean of 10",
             "gbps_per_layer_launches": round(total_bytes / (batch_ms * 1e-3) / 1e9, 1),
             "per_layer_launches": "one nf4_dequant_batch launch per layer (7 weights), 28 "
@@ -533,7 +536,12 @@ def cpu_baseline(dtype_name, reps):
 
     from oracle import nf4_oracle as o
 
-    threads = min(16, os.cpu_count() or 1)
+    # every host core this process may use: the cores the scheduler gives it (the GPU box
+    # grants one GPU's job a share of the host, which os.cpu_count() does not show) and at most
+    # the OMP_NUM_THREADS the box sets for it
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = max(1, min(avail or 1, omp if omp > 0 else (avail or 1)))
     torch.set_num_threads(threads)
     rng = np.random.default_rng(0)
     states = {}
@@ -603,6 +611,21 @@ def cpu_baseline(dtype_name, reps):
 
 # ------------------------------------------------------------------ measured device ceilings
 
+PROBE_LIB = ROOT / "kaggle-mltest_amd" / "probe" / "libnf4_probe.so"
+
+
+def _probe_lib():
+    """The bench's measurement probes (kaggle-mltest_amd/probe/nf4_probe.hip), a library of
+    their own beside the NF4 one."""
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    lib.nf4_probe_mfma.restype = ctypes.c_int
+    lib.nf4_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
+                                   ctypes.c_void_p, ctypes.c_void_p]
+    lib.nf4_probe_read.restype = ctypes.c_int
+    lib.nf4_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                   ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
 def measured_peaks(dtype, dev):
     """What this box sustains, for fractions of measured peaks beside the data-sheet ones: the
     MFMA rate of back-to-back v_mfma_f32_32x32x16 on register operands (nf4_probe_mfma, 2048
@@ -613,7 +636,7 @@ def measured_peaks(dtype, dev):
 
     from solution import _lib
 
-    lib = _lib.load()
+    lib = _probe_lib()
     dt = _lib.DTYPE_CODE[dtype]
     s = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
     ops = torch.randn(128 * 8, generator=torch.Generator().manual_seed(7)).to(dtype).to(dev)

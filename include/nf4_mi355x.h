@@ -4,8 +4,11 @@
  * The library dequantizes bitsandbytes-layout NF4 weights and multiplies with them, forward and
  * backward, on one AMD Instinct MI355X.  Every entry point takes plain device pointers, sizes, a
  * dtype code and a HIP stream (as void*), launches asynchronously on that stream and returns an
- * int status (NF4_OK == 0).  The caller allocates every output and workspace; the library owns
- * no device memory and keeps no state between calls, so it is reentrant and thread-safe.
+ * int status (NF4_OK == 0).  The caller allocates every output and workspace, and apart from
+ * one entry point the library owns no device memory and keeps no state between calls, so it is
+ * reentrant and thread-safe.  The exception is nf4_linear_dx_noalloc (for callers that cannot
+ * allocate): its split-K partials live in a 64 MiB device array that the library holds on every
+ * GPU it runs on until the process ends, and calls of it that overlap on one GPU race.
  *
  * Weight format (bitsandbytes 0.50.2 QuantState, as read by the reference at
  * /root/reference/solution/nf4.py:46-53,112-131):
@@ -29,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NF4_ABI_VERSION 2
+#define NF4_ABI_VERSION 3
 
 /* status codes */
 #define NF4_OK 0
@@ -64,7 +67,7 @@ typedef struct nf4_weight {
  * Forward reads t and b; the input-gradient GEMM reads a and da. */
 typedef struct nf4_lora {
     int32_t seg;
-    int32_t rank;          /* 1..16 */
+    int32_t rank;          /* 1..64 */
     float scale;           /* alpha / r */
     const void *t;         /* [M, rank] drop(x) @ A^T, GEMM dtype (forward) */
     const void *b;         /* [rows_seg, rank] LoRA B, GEMM dtype (forward) */
@@ -329,14 +332,16 @@ int nf4_int8_swiglu_bwd(const int32_t *acc, int64_t m, int64_t inter, int64_t ld
  * LoRA dropout (drop_mode 1 or 2) also writes the dropout inputs oq = y * keep_q * scale_q and
  * ov = y * keep_v * scale_v (scale = 1 / (1 - p)), each rounded once.  The keep masks live
  * packed: packed[r][0][j] bit k = keep_q of element 8 j + k, packed[r][1][j] the same for v
- * ([rows][2][cols / 8] bytes).  Mode 1 reads one-byte 0/1 masks keep_q, keep_v [*, cols]
- * (8-byte aligned) at row src_rows[r] (row r when src_rows is NULL: the token's row of masks
- * drawn over a padded batch) and writes their bits to packed; mode 2 reads packed.
+ * ([rows][2][cols / 8] bytes).  Mode 1 reads one-byte 0/1 masks keep_q, keep_v [keep_rows,
+ * cols] (8-byte aligned) at row src_rows[r] (row r when src_rows is NULL, which needs
+ * keep_rows >= rows: the token's row of masks drawn over a padded batch) and writes their bits
+ * to packed; a src_rows entry outside [0, keep_rows) reads as all dropped.  Mode 2 reads
+ * packed.
  * Replaces: add_rmsnorm_fwd_kernel with _pack_bits / _unpack_bits
  *           (/root/reference/solution/layer.py:76-132). */
 int nf4_add_rmsnorm(const void *x, int res_dtype, const void *d, const float *w, void *y,
                     float *rstd, const uint8_t *keep_q, const uint8_t *keep_v,
-                    const int64_t *src_rows, uint8_t *packed, int drop_mode, float scale_q,
+                    const int64_t *src_rows, int64_t keep_rows, uint8_t *packed, int drop_mode, float scale_q,
                     float scale_v, void *oq, void *ov, int64_t rows, int64_t cols, float eps,
                     int dtype, void *stream);
 
@@ -385,20 +390,6 @@ int nf4_swiglu_bwd(const void *grad, int64_t ld_h, const void *gate, const void 
  * (nf4.py:100-101). */
 int nf4_bias_grad(const void *dy, int64_t m, int64_t n, int64_t lddy, float *out, int dtype,
                   void *stream);
-
-/* ------------------------------------------------------------------ measurement probes */
-
-/* No counterpart in the reference: measurements of what this device sustains, for the bench's
- * fractions of measured peaks beside the data-sheet ones.
- * nf4_probe_mfma: `workgroups` x 256 threads issue `iters` x 4 back-to-back
- * v_mfma_f32_32x32x16 (dtype f16 or bf16) per wave on operands read from `operands` (>= 128
- * 16-byte vectors), writing one float per thread to out (workgroups x 256 floats):
- * 2 * 32 * 32 * 16 * 4 * iters * 4 * workgroups flops per launch.
- * nf4_probe_read: reads `bytes` (a multiple of 16) from src with 16-byte loads over `workgroups`
- * x 256 threads, writing one uint32 per thread to out. */
-int nf4_probe_mfma(const void *operands, int workgroups, int64_t iters, int dtype, float *out,
-                   void *stream);
-int nf4_probe_read(const void *src, int64_t bytes, int workgroups, uint32_t *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,7 +1,9 @@
 """Build the gfx950 NF4 library: `python kaggle-mltest_amd/build.py` -> solution/libnf4_mi355x.so.
 
 Every HIP source under csrc/ is compiled for gfx950 only and linked into one shared library whose
-C ABI is declared in include/nf4_mi355x.h.  hipcc cross-compiles without a GPU.
+C ABI is declared in include/nf4_mi355x.h.  The bench's measurement probes (probe/*.hip) go into a
+library of their own, probe/libnf4_probe.so, which only bench.py loads.  hipcc cross-compiles
+without a GPU.
 """
 
 from __future__ import annotations
@@ -15,8 +17,10 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
+PROBE = HERE / "probe"
 BUILD = HERE / "_build"
 LIB = HERE / "solution" / "libnf4_mi355x.so"
+PROBE_LIB = PROBE / "libnf4_probe.so"
 ARCH = "gfx950"
 
 # -ffp-contract=off: the absmax rebuild and the dequant products are separate fp32 roundings,
@@ -48,19 +52,25 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    BUILD.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    with ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
-        objs = list(pool.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = True) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    probes = sorted(PROBE.glob("*.hip"))
+    with ThreadPoolExecutor(max_workers=min(8, len(sources) + len(probes))) as pool:
+        objs = list(pool.map(_compile, sources + probes))
+    _link(objs[: len(sources)], LIB)
+    _link(objs[len(sources):], PROBE_LIB)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
+        print(f"built {LIB} from {len(sources)} sources and {PROBE_LIB}")
     return LIB
 
 

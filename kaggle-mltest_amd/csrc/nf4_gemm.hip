@@ -13,7 +13,10 @@
 // With v_mfma_f32_32x32x16 each lane then owns one activation row m and four consecutive p,
 // so results leave as 8-byte row-major stores of Y[m, n..n+3] or dX[m, k..k+3].
 //
-// Workgroup tile BP x BM (256x256 with 8 waves, or 128x128 with 4), reduction step 64 (one NF4
+// The 256x256 forward tile of a plain projection (fwd_body_rw) has each of its 8 waves own 32
+// weight rows and dequantize them straight into its MFMA operand registers, only the
+// activation tile going through LDS.  The other tilings stage both operands in LDS:
+// workgroup tile BP x BM (256x256 with 8 waves, or 128x128 with 4), reduction step 64 (one NF4
 // absmax block along k for the forward weight), two LDS stages and two register stages.  LDS
 // tiles are rows of 64 16-bit values (128 bytes) whose 16-byte chunks are XOR-swizzled with bits
 // 1..3 of the row, so the 16 rows one 16-lane group of an MFMA fragment read hit distinct banks.
@@ -32,6 +35,7 @@
 // adds up in a fixed order (deterministic).
 
 #include <mutex>
+#include <type_traits>
 
 #include "nf4_common.h"
 
@@ -620,16 +624,17 @@ template <int BM, int WM, int TP, int TM, int NT>
 __device__ __forceinline__ void partial_lds(const GemmArgs &a, float16_t (&acc)[TP][TM],
                                             uint8_t *lds, int64_t p0, int prow0, int64_t p_end,
                                             int64_t col_off, int64_t m0, int mrow0, int split) {
-    static_assert(BM % 128 == 0 && 128 % (BM / WM) == 0, "a wave's rows lie in one half");
+    static_assert(BM % 128 == 0, "whole halves of 128 rows");
     const int lane = threadIdx.x & 63;
     const int t = threadIdx.x % NT;
     const int c = t & 63;  // the thread's chunk of a row: columns 4c .. 4c + 3
 #pragma unroll 1
     for (int h = 0; h < BM / 128; ++h) {
         __syncthreads();  // the staging tiles (h = 0) or the previous half's reads are done
-        if (mrow0 / 128 == h) {
+        {
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
+                if ((mrow0 + j * 32) / 128 != h) continue;  // the fragment lies in the other half
                 const int m = mrow0 - 128 * h + j * 32 + (lane & 31);
 #pragma unroll
                 for (int i = 0; i < TP; ++i)
@@ -1161,6 +1166,197 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
     }
 }
 
+// Row-owning main loop of a 256x256 forward tile: wave w (of 8) owns the 32 weight rows
+// p0 + 32 w .. and all 256 activation rows of the tile, and dequantizes its rows straight into
+// its MFMA A fragments: the weight tile never goes through LDS and no two waves dequantize the
+// same element.  Lane l takes row 32 w + l % 32 and the packed bytes 16 (l / 32) .. + 15 of the
+// row's 64-deep step (elements k = 32 (l / 32) + 0 .. 31, one absmax block); its A fragment of
+// k-substep ks is dword ks of those bytes (k = 32 (l / 32) + 8 ks + 0 .. 7), and its B
+// fragments read the activation chunk 4 (l / 32) + ks of their rows, the same k.  Per step s:
+// the table of step s + 1 is built and its A fragments dequantized, a quarter per k-substep,
+// among the MFMAs of step s (two A-fragment register sets); the activation tile of step s + 1
+// goes to the other LDS stage by LDS DMA and the packed bytes of step s + 2 to the free
+// register stage; one barrier.
+template <int DT>
+__device__ __forceinline__ void fwd_body_rw(const GemmArgs &a, const TileMap &tm, uint32_t blk,
+                                            uint8_t *lds, float (*s_code2)[256]) {
+    constexpr int BP = 256, BM = 256, NT = 512, TP = 1, TM = 8, NS = 2;
+    constexpr int STG = BM * ROWB;  // bytes of one activation stage
+    const BlockTile bt = block_tile(a, blk);
+    const int split = bt.split;
+    const int64_t tile = bt.tile;
+    const int seg = seg_of_tile(a, tm, tile);
+    const uint32_t local = static_cast<uint32_t>(tile - tm.tile_start[seg]);
+    const uint32_t mtl = static_cast<uint32_t>(tm.m_tiles);
+    const int64_t p0 = uniform64(tm.row0[seg] + static_cast<int64_t>(local / mtl) * BP);
+    const int64_t m0 = uniform64(static_cast<int64_t>(local % mtl) * BM);
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const DevWeight w = a.w[seg];
+    const int64_t K = a.K;
+    const int64_t steps = K / BR;
+    const int64_t per = bt.nsplit > 1 ? a.per_split : steps;
+    const int64_t s0 = uniform64(split * per);
+    const int64_t s1 = uniform64(s0 + per < steps ? s0 + per : steps);
+    const int64_t nv = s1 - s0;
+
+    const int ci = static_cast<int>(threadIdx.x);
+    const uint32_t c2a = bload4(make_rsrc(a.w[seg].code2, a.w[seg].nested ? 1024 : 0), ci * 4);
+    const float *code2 = s_code2[0];
+    float code_r[16];
+    load_code_sgpr(w.code, code_r);
+    const int lane = threadIdx.x & 63;
+    const int r32 = lane & 31, kh = lane >> 5;
+    const int prow0 = wave * 32;
+
+    float16_t acc[TP][TM];
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[0][j] = (float16_t){};
+
+    // this lane's 16 packed bytes and absmax block of step 0 (rows past the weight read zero)
+    const WeightRsrc wr = weight_rsrc(w);
+    const int64_t wrow = p0 + prow0 + r32;
+    const int wpk = static_cast<int>(wrow * (K >> 1) + kh * 16);
+    const int wblk = static_cast<int>(wrow * (K >> wr.bs_shift));
+    struct Raw {
+        u32x4_t raw;
+        AbsIn abs;
+    };
+    auto wload = [&](Raw &r, int64_t u) {
+        const int st = static_cast<int>(s0 + u);
+        r.raw = bload16(wr.packed, wpk + st * (BR / 2));
+        r.abs = absmax_bload(wr, wblk + ((st * BR) >> wr.bs_shift));
+    };
+    const rsrc_t ar = act_rsrc<BM>(a, m0);
+    // activation DMA: wave w sends rows 32 w .. 32 w + 31 (4 blocks of 8 rows), lane i writing
+    // position i & 7 of row i >> 3 of a block (swz layout)
+    int adoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = (wave * 4 + j) * 8 + (lane >> 3);
+        adoff[j] = row * static_cast<int>(a.ld_act) * 2 + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
+    }
+    const uint32_t lds_a =
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t *)lds)) +
+        wave * 32 * ROWB;
+    auto dma_a = [&](int b, int64_t u) {
+        const int kb = static_cast<int>(s0 + u) * (BR * 2);
+        const uint32_t base = __builtin_amdgcn_readfirstlane(lds_a + b * STG);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                         :
+                         : "s"(base + j * 8 * ROWB), "v"(adoff[j]), "s"(ar), "s"(kb)
+                         : "memory", "m0");
+        }
+    };
+    // Every DMA is followed by exactly one register stage's 3 loads before this wait.
+    auto wait_dma = [] { asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); };
+
+    Raw rs[2] = {};
+    if (nv > 0) {
+        dma_a(0, 0);
+        wload(rs[0], 0);
+        wload(rs[1], 1);
+    }
+
+    const LoraDev &lo = a.lora[seg];
+    if (lo.has && split == 0) {
+        const int kq = kh * 8;
+        for (int k0 = 0; k0 < lo.rank; k0 += 16) {
+            const int lim = lo.rank - (k0 + kq);
+            u32x4_t fa, fb[TM];
+            {
+                const int64_t p = p0 + prow0 + r32;
+                fa = (p < w.rows && lim > 0) ? lora_row8(lo.b + p * lo.rank + k0 + kq, lim, lo.vec)
+                                             : (u32x4_t){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int64_t m = m0 + j * 32 + r32;
+                fb[j] = (m < a.M && lim > 0) ? lora_row8(lo.t + m * lo.rank + k0 + kq, lim, lo.vec)
+                                             : (u32x4_t){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc[0][j] = mfma32<DT>(fa, fb[j], acc[0][j]);
+        }
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc[0][j] *= lo.scale;
+    }
+
+    if (ci < 256) s_code2[0][ci] = a.w[seg].nested ? __builtin_bit_cast(float, c2a) : (ci == 0 ? 1.0f : 0.0f);
+    __syncthreads();  // tables
+
+    auto dword = [](const u32x4_t &v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; };
+    // B fragment of k-substep ks, m fragment j, from activation stage b
+    auto bfrag = [&](int b, int ks, int j) {
+        return *reinterpret_cast<const u32x4_t *>(lds + b * STG + swz(j * 32 + r32, kh * 4 + ks));
+    };
+    // A fragments: fa[ks] holds k-substep ks of the current step until that substep's MFMAs are
+    // issued, then the next step's (one register set)
+    u32x4_t fa[4];
+    if (nv > 0) {
+        const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, rs[0].abs, code2));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) fa[q] = lookup8(tb, dword(rs[0].raw, q));
+        wload(rs[0], 2);
+        wait_dma();
+        __syncthreads();
+        // Step v from LDS stage B = v & 1 (B a constant: the loop runs two steps per pass); the
+        // next step's fragments from register stage B ^ 1 (step v + 1), whose loads of step v + 3
+        // follow its last use; the DMA of step v + 1 into stage B ^ 1 after the first k-substep.
+        int64_t v = 0;
+        auto body = [&](auto bc) {
+            constexpr int B = decltype(bc)::value;
+            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, rs[B ^ 1].abs, code2));
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                u32x4_t fb[TM];
+#pragma unroll
+                for (int j = 0; j < TM; ++j) fb[j] = bfrag(B, ks, j);
+#pragma unroll
+                for (int j = 0; j < TM; ++j) acc[0][j] = mfma32<DT>(fa[ks], fb[j], acc[0][j]);
+                fa[ks] = lookup8(tb, dword(rs[B ^ 1].raw, ks));
+                if (ks == 0) dma_a(B ^ 1, v + B + 1);
+                if (ks == 3) wload(rs[B ^ 1], v + B + 3);
+                __builtin_amdgcn_sched_barrier(0);  // one k-substep's work at a time
+            }
+            wait_dma();
+            __syncthreads();
+        };
+        for (; v + 1 < nv; v += 2) {
+            body(std::integral_constant<int, 0>{});
+            body(std::integral_constant<int, 1>{});
+        }
+        if (v < nv) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                u32x4_t fb[TM];
+#pragma unroll
+                for (int j = 0; j < TM; ++j) fb[j] = bfrag(0, ks, j);
+#pragma unroll
+                for (int j = 0; j < TM; ++j) acc[0][j] = mfma32<DT>(fa[ks], fb[j], acc[0][j]);
+            }
+        }
+    }
+    if (a.vec16_out && bt.nsplit == 1 && !a.bias && !a.accumulate) {
+        epilogue_lds<DT, BP, BM, TP, TM, NT>(a, acc, lds, p0, prow0, w.rows, a.seg_off[seg], m0, 0);
+        return;
+    }
+    if (bt.nsplit > 1 && a.tail_cols % 4 == 0 && (a.seg_off[seg] - a.tail_col0) % 4 == 0) {
+        partial_lds<BM, 1, TP, TM, NT>(a, acc, lds, p0, prow0, w.rows, a.seg_off[seg], m0, 0, split);
+        return;
+    }
+    epilogue<DT, TP, TM>(a, acc, p0 + prow0, w.rows, a.seg_off[seg], m0, split, bt.nsplit > 1);
+}
+
+template <int DT>
+__global__ __launch_bounds__(512) void fwd_rw_kernel(const GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
+    __shared__ float s_code2[1][256];
+    fwd_body_rw<DT>(a, a.map[0], blockIdx.x, lds, s_code2);
+}
+
+
 template <int DT, int BP, int BM, int WP, int WM, int EPI = 0, int KG = 1>
 __global__ __launch_bounds__(KG *WP *WM * 64) void fwd_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<BP, BM, KG>()];
@@ -1177,9 +1373,10 @@ __global__ __launch_bounds__(512) void fwd_head_tail_kernel(const GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[stage_bytes<256, 256, 1>()];
     __shared__ float s_code2[EPI != 0 ? 2 : 1][256];
     const uint32_t b0 = static_cast<uint32_t>(a.blocks0);
-    if (blockIdx.x < b0)
-        fwd_body<DT, 256, 256, 2, 4, EPI, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
-    else
+    if (blockIdx.x < b0) {
+        if constexpr (EPI == 0) fwd_body_rw<DT>(a, a.map[0], blockIdx.x, lds, s_code2);
+        else fwd_body<DT, 256, 256, 2, 4, EPI, 1>(a, a.map[0], blockIdx.x, lds, s_code2);
+    } else
         fwd_body<DT, 128, 128, 2, 2, EPI, 2>(a, a.map[1], blockIdx.x - b0, lds, s_code2);
 }
 
@@ -2081,6 +2278,7 @@ constexpr int64_t kGemvMaxM = 32;
 
 constexpr int kCUs = 256;
 
+
 int fill_common(GemmArgs &g, const void *act, int64_t m, int64_t ld_act, const nf4_weight *ws,
                 int nw) {
     if (!ws || nw < 1 || nw > kMaxSeg) return NF4_ERR_ARG;
@@ -2341,8 +2539,9 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
         if (p.waves == 16) hipLaunchKernelGGL((gemv_kernel<DT, 1, 16>), grid, block, 0, st, g);
         else if (p.waves == 8) hipLaunchKernelGGL((gemv_kernel<DT, 1, 8>), grid, block, 0, st, g);
         else hipLaunchKernelGGL((gemv_kernel<DT, 1, 4>), grid, block, 0, st, g);
-    } else if (p.cfg == 0)
-        hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4>), grid, dim3(512), 0, st, g);
+    } else if (p.cfg == 0) {
+        hipLaunchKernelGGL((fwd_rw_kernel<DT>), grid, dim3(512), 0, st, g);
+    }
     else if (p.cfg == 3)
         hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2, 0, 2>), grid, dim3(512), 0, st, g);
     else
@@ -2353,8 +2552,9 @@ int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
 template <int DT, int EPI>
 int launch_paired(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
-    if (p.cfg == 0)
+    if (p.cfg == 0) {
         hipLaunchKernelGGL((fwd_kernel<DT, 256, 256, 2, 4, EPI>), grid, dim3(512), 0, st, g);
+    }
     else if (p.cfg == 3)
         hipLaunchKernelGGL((fwd_kernel<DT, 128, 128, 2, 2, EPI, 2>), grid, dim3(512), 0, st, g);
     else

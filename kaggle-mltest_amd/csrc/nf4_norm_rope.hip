@@ -111,6 +111,7 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 struct NormDrop {
     const uint8_t *keep_q, *keep_v;  // mode 1: one byte per element, rows src_rows[r] (or r)
     const int64_t *src_rows;
+    int64_t keep_rows;               // mode 1: rows of keep_q / keep_v
     uint8_t *packed;                 // [rows][2][cols / 8]: q's bits, then v's
     int mode;                        // 0 none, 1 pack from keep_q / keep_v, 2 read packed
     float scale_q, scale_v;
@@ -149,6 +150,8 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
     if (threadIdx.x == 0) rstd_out[row] = rstd;
     const int64_t src = drop.mode == 1 && drop.src_rows ? drop.src_rows[row] : row;
+    // a mask row outside keep_q / keep_v (a bad row map) is read as all dropped, never fetched
+    const bool src_ok = src >= 0 && src < drop.keep_rows;
     uint8_t *bits = drop.mode != 0 ? drop.packed + row * 2 * chunks : nullptr;
 #pragma unroll
     for (int c = 0; c < kNormChunks; ++c) {
@@ -161,8 +164,8 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
         if (drop.mode != 0) {
             uint32_t bq, bv;
             if (drop.mode == 1) {
-                bq = pack8(drop.keep_q + src * cols + ch * 8);
-                bv = pack8(drop.keep_v + src * cols + ch * 8);
+                bq = src_ok ? pack8(drop.keep_q + src * cols + ch * 8) : 0u;
+                bv = src_ok ? pack8(drop.keep_v + src * cols + ch * 8) : 0u;
                 bits[ch] = static_cast<uint8_t>(bq);
                 bits[chunks + ch] = static_cast<uint8_t>(bv);
             } else {
@@ -516,16 +519,18 @@ int rope_shape_ok(int64_t tokens, int n_heads, int n_kv, int head_dim, int dtype
 
 extern "C" int nf4_add_rmsnorm(const void *x, int res_dtype, const void *d, const float *w,
                                void *y, float *rstd, const uint8_t *keep_q,
-                               const uint8_t *keep_v, const int64_t *src_rows, uint8_t *packed,
-                               int drop_mode, float scale_q, float scale_v, void *oq, void *ov,
-                               int64_t rows, int64_t cols, float eps, int dtype, void *stream) {
+                               const uint8_t *keep_v, const int64_t *src_rows, int64_t keep_rows,
+                               uint8_t *packed, int drop_mode, float scale_q, float scale_v,
+                               void *oq, void *ov, int64_t rows, int64_t cols, float eps,
+                               int dtype, void *stream) {
     int st = norm_shape_ok(rows, cols, dtype);
     if (st != NF4_OK) return st;
     if (res_dtype != dtype && res_dtype != NF4_F32) return NF4_ERR_ARG;
     if (rows > 0 && (!x || !w || !y || !rstd)) return NF4_ERR_ARG;
     if (drop_mode < 0 || drop_mode > 2) return NF4_ERR_ARG;
     if (drop_mode != 0 && (!packed || !oq || !ov)) return NF4_ERR_ARG;
-    if (drop_mode == 1 && (!keep_q || !keep_v)) return NF4_ERR_ARG;
+    if (drop_mode == 1 && (!keep_q || !keep_v || keep_rows < 0)) return NF4_ERR_ARG;
+    if (drop_mode == 1 && !src_rows && keep_rows < rows) return NF4_ERR_ARG;  // masks row r
     for (const void *p : {x, d, static_cast<const void *>(y), static_cast<const void *>(oq),
                           static_cast<const void *>(ov)})
         if (p && !aligned(p, 16)) return NF4_ERR_UNSUPPORTED;
@@ -534,7 +539,7 @@ extern "C" int nf4_add_rmsnorm(const void *x, int res_dtype, const void *d, cons
     if (rows > 0x7fffffff) return NF4_ERR_ARG;
     auto s = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(rows));
-    const NormDrop dr{keep_q, keep_v, src_rows, packed, drop_mode, scale_q, scale_v};
+    const NormDrop dr{keep_q, keep_v, src_rows, keep_rows, packed, drop_mode, scale_q, scale_v};
     auto D = static_cast<const uint16_t *>(d);
     auto Y = static_cast<uint16_t *>(y), Q = static_cast<uint16_t *>(oq), V = static_cast<uint16_t *>(ov);
 #define NF4_NORM_FWD(DT, RT)                                                                       \

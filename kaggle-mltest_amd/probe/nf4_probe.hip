@@ -1,8 +1,16 @@
-// Measurement kernels: what this device sustains, for fractions of measured peaks beside the
-// data-sheet ones (the MFMA rate on register operands, the HBM read rate).  No counterpart in
-// the reference; nothing on the NF4 path calls them.
+// Measurement kernels of bench.py (built into libnf4_probe.so, not the NF4 library): what this
+// device sustains, for fractions of measured peaks beside the data-sheet ones (the MFMA rate on
+// register operands, the HBM read rate).  No counterpart in the reference.
+//
+//   nf4_probe_mfma(operands, workgroups, iters, dtype, out, stream): `workgroups` x 256 threads
+//     issue `iters` x 4 back-to-back v_mfma_f32_32x32x16 (dtype 0 f16, 1 bf16) per wave on
+//     operands read from `operands` (>= 128 16-byte vectors), one float per thread to out:
+//     2 * 32 * 32 * 16 * 4 * iters * 4 * workgroups flops per launch.
+//   nf4_probe_read(src, bytes, workgroups, out, stream): reads `bytes` (a multiple of 16) with
+//     16-byte loads over `workgroups` x 256 threads, one uint32 per thread to out.
+// Both return 0, or nonzero for bad arguments or a launch error.
 
-#include "nf4_common.h"
+#include "../csrc/nf4_common.h"
 
 namespace {
 

@@ -102,8 +102,6 @@ _SIGNATURES = {
                                   c_void_p]),
     "nf4_lora_ax_multi": (c_int, [ctypes.POINTER(NF4LoraJob), c_int, c_int64, c_int, c_int,
                                   c_void_p]),
-    "nf4_probe_mfma": (c_int, [c_void_p, c_int, c_int64, c_int, c_void_p, c_void_p]),
-    "nf4_probe_read": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p]),
     "nf4_lora_wgrad_multi": (c_int, [ctypes.POINTER(NF4LoraJob), c_int, c_int64, c_int, c_int,
                                      c_void_p, c_size_t, c_void_p]),
     "nf4_lora_wgrad_multi_workspace": (c_size_t, [ctypes.POINTER(NF4LoraJob), c_int, c_int64,
@@ -130,8 +128,9 @@ _SIGNATURES = {
                                     c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int,
                                     c_void_p]),
     "nf4_add_rmsnorm": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
-                                c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_float, c_float,
-                                c_void_p, c_void_p, c_int64, c_int64, c_float, c_int, c_void_p]),
+                                c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int, c_float,
+                                c_float, c_void_p, c_void_p, c_int64, c_int64, c_float, c_int,
+                                c_void_p]),
     "nf4_rmsnorm_bwd": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_float, c_float,
                                 c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_int64, c_int64, c_int, c_void_p]),

@@ -155,6 +155,9 @@ def linear_dx(dy: torch.Tensor, weights, loras=(), out: torch.Tensor | None = No
     if out is None:
         out = torch.empty((m, k), dtype=dy.dtype, device=dy.device)
         accumulate = False
+    offs = _offsets(weights)
+    if tile is None and len(weights) > 1 and any(o % 8 for o in offs):
+        return _linear_dx_by_segment(dy, weights, loras, out, accumulate, offs)
     arr = _descs(weights)
     lib = load()
     if tile is None:
@@ -170,6 +173,35 @@ def linear_dx(dy: torch.Tensor, weights, loras=(), out: torch.Tensor | None = No
         check(lib.nf4_linear_dx(*args), "nf4_linear_dx")
     else:
         check(lib.nf4_linear_dx_tiled(*args, int(tile), int(splits)), "nf4_linear_dx_tiled")
+    return out
+
+
+def _offsets(weights):
+    offs, o = [], 0
+    for _, qs in weights:
+        offs.append(o)
+        o += int(qs.shape[0])
+    return offs
+
+
+def _linear_dx_by_segment(dy, weights, loras, out, accumulate, offs):
+    """linear_dx over stacked segments of which one starts off a multiple of 8 dY columns: the
+    stacked launch reads each segment's dY columns as 16-byte chunks, so each segment runs as
+    its own launch over its dY columns (copied when they are not 16-byte aligned), the first
+    writing dX and the others adding to it; a LoRA struct goes with its segment's launch."""
+    by_seg = {}
+    for lo in loras:
+        by_seg.setdefault(int(lo.seg), []).append(lo)
+    for i, (w, off) in enumerate(zip(weights, offs)):
+        rows = int(w[1].shape[0])
+        dy_s = dy[:, off: off + rows]
+        if dy_s.data_ptr() % 16 or dy_s.stride(0) % 8:  # to rows of a multiple of 8 values
+            pad = torch.empty((dy.shape[0], -(-rows // 8) * 8), dtype=dy.dtype, device=dy.device)
+            pad[:, :rows].copy_(dy_s)
+            dy_s = pad[:, :rows]
+        seg_loras = [NF4Lora(seg=0, rank=lo.rank, scale=lo.scale, t=lo.t, b=lo.b, a=lo.a, da=lo.da)
+                     for lo in by_seg.get(i, [])]
+        linear_dx(dy_s, [w], seg_loras, out=out, accumulate=accumulate or i > 0)
     return out
 
 
@@ -372,8 +404,10 @@ def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, d: torch.Tensor | 
         mode = 2
     if mode:
         oq, ov = torch.empty_like(y), torch.empty_like(y)
+    keep_rows = int(kq.shape[0]) if kq is not None else 0
     st = load().nf4_add_rmsnorm(_p(x), DTYPE_CODE[x.dtype], _p(d), _p(w), _p(y), _p(rstd), _p(kq),
-                                _p(kv), _p(rows) if mode == 1 else None, _p(packed), mode,
+                                _p(kv), _p(rows) if mode == 1 else None, keep_rows, _p(packed),
+                                mode,
                                 float(scale_q), float(scale_v), _p(oq), _p(ov), n, cols,
                                 float(eps), _code(dtype), stream_of(x))
     check(st, "nf4_add_rmsnorm")

@@ -208,9 +208,9 @@ class NF4Projection(torch.autograd.Function):
             rows = int(spec.weights[ad.seg][1].shape[0])
             dy_s = dy[:, offs[ad.seg]: offs[ad.seg] + rows]
             if dy_s.data_ptr() % 16:
-                dy_s = dy_s.contiguous()
+                dy_s = dy_s.contiguous()  # a copy only the job structs point to
             da = torch.empty((x.shape[0], r), dtype=x.dtype, device=x.device)
-            live.append(da)
+            live += [dy_s, da]
             grad_b = torch.empty((rows, r), dtype=torch.float32, device=x.device)
             grad_a = torch.empty((r, x.shape[1]), dtype=torch.float32, device=x.device)
             da_jobs.append((r, kernels.lora_job(dy_s, b16, da, ad.scale)))

@@ -95,7 +95,7 @@ def test_dma_is_waited_for_before_the_barrier(tmp_path):
     res = subprocess.run(cmd, capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-2000:]
     kernels = [(k, b) for k, b in _kernels(out.read_text())
-               if re.search(r"(fwd|dx)_(head_tail_)?kernel", k)]
+               if re.search(r"(fwd|dx)_(head_tail_|rw_)?kernel", k)]
     assert len(kernels) >= 8
     checked = 0
     for name, body in kernels:

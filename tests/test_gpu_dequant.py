@@ -232,3 +232,21 @@ def test_table_bit_exact(cuda, dt):
     torch.cuda.synchronize()
     assert all(not out.any() for out in table.outs)
     assert lib.nf4_dequant_table(table.table.data_ptr(), 0, table.blocks, table._code, s) != 0
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_table_qwen15b_layer_bit_exact(cuda, dt):
+    """The timed dequant at its workload: one nf4_dequant_table launch over a whole
+    Qwen2.5-1.5B decoder layer (q, k, v, o, gate, up, down at their real shapes, 46.8 M
+    elements, each weight quantized on its own: distinct packed bytes, absmax codes and absmax2
+    scales, as in the bench's 28-layer stack), every output bit-exact against the oracle."""
+    from solution import kernels
+
+    banner("dequant table, Qwen2.5-1.5B layer", dt)
+    layer = [(1536, 1536), (256, 1536), (256, 1536), (1536, 1536), (8960, 1536), (8960, 1536),
+             (1536, 8960)]
+    ws = [random_weight(n, k, seed=1000 + i, dev=cuda) for i, (n, k) in enumerate(layer)]
+    table = kernels.DequantTable(ws, DT[dt])
+    table.run()
+    for (p, qs), out in zip(ws, table.outs):
+        assert torch.equal(_bits(out).reshape(-1), _oracle(p, qs, dt).reshape(-1)), tuple(qs.shape)

@@ -477,3 +477,45 @@ def test_rows_decode_long_and_odd_rows(cuda, m, n, k):
     bias = _x(1, n, 15, cuda, std=0.1).view(-1)
     y = kernels.linear_fwd(x, [(p, qs)], bias)
     assert_rel(y, o.linear_fwd(x, oracle_w16(p, qs), bias), what=f"M={m} {n}x{k}")
+
+
+@pytest.mark.parametrize("r", [1, 8, 17, 32, 48, 64])
+@pytest.mark.parametrize("tile", [None, 0, 1, 3])
+def test_lora_slab_ranks(cuda, r, tile):
+    """The LoRA slabs of the fused forward and input-gradient GEMMs at ranks 1..64 (the ABI's
+    range): the slab runs the rank in 16-deep MFMA chunks with the ranks past r masked, so
+    ranks that are not a multiple of 16 and several chunks are the cases; every tiling.  The
+    LoRA term is made large (B ~ N(0, 0.2)) so that it is checked on its own as well."""
+    from solution import kernels
+
+    banner("lora slab rank", r, "tile", tile)
+    m, k, s = 300, 512, 0.5
+    rows = (320, 64, 64)
+    segs = [random_weight(n, k, seed=500 + i, dev=cuda) for i, n in enumerate(rows)]
+    w = torch.cat([oracle_w16(p, q) for p, q in segs])
+    x = _x(m, k, 11, cuda)
+    g = torch.Generator().manual_seed(12)
+    a0 = ((torch.rand(r, k, generator=g) * 2 - 1) / np.sqrt(k)).half().to(cuda)
+    a2 = ((torch.rand(r, k, generator=g) * 2 - 1) / np.sqrt(k)).half().to(cuda)
+    b0 = (torch.randn(rows[0], r, generator=g) * 0.2).half().to(cuda)
+    b2 = (torch.randn(rows[2], r, generator=g) * 0.2).half().to(cuda)
+    t0, t2 = kernels.lora_xa(x, a0), kernels.lora_xa(x, a2)
+    loras = [kernels.make_lora(0, r, s, t=t0, b=b0), kernels.make_lora(2, r, s, t=t2, b=b2)]
+    y = kernels.linear_fwd(x, segs, None, loras, tile=tile)
+    spec = [(0, rows[0], x, a0, b0, s), (rows[0] + rows[1], rows[2], x, a2, b2, s)]
+    ref = o.linear_fwd(x, w, None, spec)
+    assert_rel(y, ref, what=f"fwd r={r}")
+    base = o.linear_fwd(x, w)
+    assert_rel((y.float().cpu() - base)[:, :rows[0]], (ref - base)[:, :rows[0]], max_rel=5e-2,
+               mean_rel=5e-2, what=f"lora part r={r}")
+
+    dy = _x(m, sum(rows), 13, cuda, std=1e-2)
+    da0 = kernels.lora_da(dy[:, :rows[0]], b0, s)
+    da2 = kernels.lora_da(dy[:, rows[0] + rows[1]:], b2, s)
+    dl = [kernels.make_lora(0, r, s, a=a0, da=da0), kernels.make_lora(2, r, s, a=a2, da=da2)]
+    dx = kernels.linear_dx(dy, segs, dl, tile=tile)
+    ref_dx = o.linear_dx(dy, w, spec)
+    assert_rel(dx, ref_dx, what=f"dx r={r}")
+    base_dx = o.linear_dx(dy, w)
+    assert_rel(dx.float().cpu() - base_dx, ref_dx - base_dx, max_rel=5e-2, mean_rel=5e-2,
+               what=f"dx lora part r={r}")

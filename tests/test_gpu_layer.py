@@ -202,3 +202,44 @@ def test_projection_backward_with_dirty_allocator_cache(cuda):
         assert_rel(x.grad, xr.grad, what="dx")
         for name, p, ref in zip(("dA_q", "dB_q", "dA_v", "dB_v"), params, leaves):
             assert_rel(p.grad, ref.grad, what=name)
+
+
+def test_projection_backward_misaligned_lora_segments(cuda):
+    """Two adapters on segments whose dY columns start off a 16-byte boundary (segment rows
+    4, 98, 42: offsets 4 and 102): the backward copies each adapter's dY slice, and those copies
+    are reached only through the job structs, so they must outlive the loop that makes them.
+    The allocator cache is filled with NaN first, so a copy freed early and handed to the next
+    allocation shows in dA / dB."""
+    from solution.layer import LoraAdapter, ProjectionSpec, project
+
+    banner("NF4Projection backward, adapters on misaligned dY segments")
+    m, k, r, s = 384, 512, 16, 2.0
+    rows = (4, 98, 42)
+    segs = [random_weight(n, k, seed=300 + i, dev=cuda) for i, n in enumerate(rows)]
+    w = torch.cat([oracle_w16(pp, q) for pp, q in segs]).float()
+    g = torch.Generator().manual_seed(11)
+    x0 = torch.randn(m, k, generator=g).half()
+    dy = (torch.randn(m, sum(rows), generator=g) * 1e-3).half()
+    params0 = [(torch.rand(r, k, generator=g) - 0.5) * 0.05, torch.randn(rows[1], r, generator=g) * 0.01,
+               (torch.rand(r, k, generator=g) - 0.5) * 0.05, torch.randn(rows[2], r, generator=g) * 0.01]
+    spec = ProjectionSpec(weights=segs, loras=[LoraAdapter(1, s), LoraAdapter(2, s)])
+    xr = x0.float().requires_grad_()
+    leaves = [p.clone().requires_grad_() for p in params0]
+    a1, b1, a2, b2 = leaves
+    yr = xr @ w.t()
+    o1, o2 = rows[0], rows[0] + rows[1]
+    yr = torch.cat([yr[:, :o1], yr[:, o1:o2] + s * (xr @ a1.t()) @ b1.t(),
+                    yr[:, o2:] + s * (xr @ a2.t()) @ b2.t()], -1)
+    yr.backward(dy.float())
+    for _ in range(3):
+        torch.full((1 << 26,), float("nan"), dtype=torch.float16, device=cuda)  # freed at once
+        x = x0.to(cuda).requires_grad_()
+        params = [p.to(cuda).requires_grad_() for p in params0]
+        y = project(x, spec, None, params)
+        assert_rel(y, yr.detach(), what="y")
+        torch.full((1 << 26,), float("nan"), dtype=torch.float16, device=cuda)
+        y.backward(dy.to(cuda))
+        torch.cuda.synchronize()
+        assert_rel(x.grad, xr.grad, what="dx")
+        for name, p, ref in zip(("dA_1", "dB_1", "dA_2", "dB_2"), params, leaves):
+            assert_rel(p.grad, ref.grad, what=name)

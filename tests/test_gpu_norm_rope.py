@@ -158,3 +158,30 @@ def test_norm_rope_arguments(cuda):
     cos = torch.ones(2, 64, device=cuda)
     with pytest.raises(Exception):
         kernels.qkv_rope(qkv, cos, cos, 3, 2, 64)  # 3 heads do not group over 2 kv heads
+
+
+def test_add_rmsnorm_row_map_out_of_range(cuda):
+    """A token -> mask-row map entry outside the masks' rows (negative or past the last) reads
+    nothing: that token's masks count as all dropped (zero bits, zero dropout inputs) while the
+    others match the in-range gather bit for bit."""
+    from solution import kernels
+
+    banner("rmsnorm fwd, row map out of range")
+    rows, cols, dtype = 6, 256, torch.float16
+    x = _r((rows, cols), 21, cuda, torch.float32)
+    w = (torch.rand(cols, generator=torch.Generator().manual_seed(22)) + 0.5).to(cuda)
+    kq, kv = _keep((4, cols), 23, cuda), _keep((4, cols), 24, cuda)
+    src = torch.tensor([3, 0, 4, 1, -1, 1000], dtype=torch.int64, device=cuda)
+    y, _, oq, ov, packed = kernels.add_rmsnorm(x, w, 1e-6, dtype=dtype, keep_q=kq, keep_v=kv,
+                                               rows=src, scale_q=2.0, scale_v=2.0)
+    ok = torch.tensor([3, 0, 1, 1])
+    y2, _, oq2, ov2, packed2 = kernels.add_rmsnorm(x[[0, 1, 3, 3]].contiguous(), w, 1e-6,
+                                                   dtype=dtype, keep_q=kq, keep_v=kv,
+                                                   rows=ok.to(cuda), scale_q=2.0, scale_v=2.0)
+    for mine, other in ((0, 0), (1, 1), (3, 2)):
+        assert torch.equal(packed[mine], packed2[other])
+        assert torch.equal(oq[mine], oq2[other]) and torch.equal(ov[mine], ov2[other])
+    for bad in (2, 4, 5):
+        assert not packed[bad].any() and not oq[bad].any() and not ov[bad].any()
+        assert torch.equal(y[bad], kernels.add_rmsnorm(x[bad:bad + 1].contiguous(), w, 1e-6,
+                                                       dtype=dtype)[0][0])
