@@ -1538,6 +1538,182 @@ void decode_kernel(const GemmArgs a) {
     if (wave == 0) epilogue16<DT>(a, acc, p0 + 4 * g, w.rows, a.seg_off[seg], r);
 }
 
+// ------------------------------------------------------------------ skinny forward path
+//
+// Y = X W^T for 2 < M <= 64 tokens (decode steps and small batches) with K a multiple of 128,
+// on v_mfma_f32_16x16x32: A = 16 weight rows dequantized straight into registers, B = 16
+// tokens.  A workgroup of RT x KP waves owns 16 RT weight rows of one segment: wave w takes the
+// 16-row tile w % RT and the k-part w / RT (KP contiguous ranges of 128-deep super-steps).
+// The activations, the one operand all of a workgroup's row tiles share, are read from memory
+// once per workgroup into LDS: in round r the stage holds, for each k-part kp, its super-step
+// kp * per + r for the 16 MT tokens ([KP][16 MT][128 k], two stages, loaded through registers
+// one round ahead by every thread, token rows >= M reading zero), and each wave reads its MT B
+// fragments per k-substep from there.  (One workgroup per 16 rows, each reading all of X from
+// L2, moved twice the weight bytes at M = 8.)  Lane l takes row 16 rt + l % 16 and the k values
+// 32 (l / 16) .. + 31 of a super-step (16 packed bytes, one absmax block); k-substep ks uses
+// 32 (l / 16) + 8 ks .. + 7, and the B fragment of token group mt the same k of token
+// 16 mt + l % 16 (LDS rows of 256 bytes, 16-byte chunk c of token t at c ^ (t % 16), so the 16
+// tokens of a fragment read hit 16 distinct bank groups).  A wave past the end of its k-part
+// (the last part may be shorter) skips the arithmetic of a round but keeps loading and meeting
+// the barriers.  The KP partial tiles are added in k-part order through LDS (deterministic).
+constexpr int64_t kSkinnyMaxM = 64;
+
+template <int DT, int MT, int RT, int KP>
+__global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) {
+    constexpr int NW = RT * KP, NT = NW * 64, MP = 16 * MT;
+    constexpr int WS = 3;                 // weight register stages
+    constexpr int XROW = DK * 2;          // LDS bytes of one token's super-step
+    constexpr int XSTG = KP * MP * XROW;  // one activation stage
+    constexpr int XCH = XSTG / 16;        // its 16-byte chunks
+    constexpr int CH = (XCH + NT - 1) / NT;
+    static_assert(2 * XSTG + 1024 <= 160 * 1024, "two activation stages fit in LDS");
+    static_assert((KP - 1) * RT * MT * 64 * 16 <= 2 * XSTG, "the k-part sums fit in the stages");
+    __shared__ __attribute__((aligned(16))) uint8_t s_x[2 * XSTG];
+    __shared__ float s_code2[256];
+
+    const int64_t tile = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(blockIdx.x));
+    const int seg = seg_of_tile(a, a.map[0], tile);
+    const int64_t p0 = uniform64((tile - a.map[0].tile_start[seg]) * (16 * RT));
+    const DevWeight w = a.w[seg];
+    const int64_t K = a.K;
+    const int ss = static_cast<int>(K / DK);
+    const int per = (ss + KP - 1) / KP;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int rt = wave % RT, kp = wave / RT;
+    const int my0 = kp * per;
+    const int my_n = ss - my0 < per ? (ss - my0 > 0 ? ss - my0 : 0) : per;
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+
+    for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = code2_entry(w, i);
+    float code_r[16];
+    load_code_sgpr(w.code, code_r);
+
+    // weights: 16 packed bytes of this lane's row per super-step; a wave's loads past its part
+    // repeat its last super-step (cached bytes, never used)
+    const WeightRsrc wr = weight_rsrc(w);
+    const int64_t row = p0 + 16 * rt + r;
+    const int wpk = static_cast<int>(row * (K >> 1) + 16 * g);
+    const int wblk = static_cast<int>(row * (K >> wr.bs_shift));
+    const int last = my_n > 0 ? my0 + my_n - 1 : 0;
+    struct WStage {
+        u32x4_t raw;
+        AbsIn abs;
+    };
+    auto wload = [&](WStage &s, int v) {
+        const int st = my0 + v < last ? my0 + v : last;
+        s.raw = bload16(wr.packed, wpk + st * (DK / 2));
+        s.abs = absmax_bload(wr, wblk + ((st * DK + 32 * g) >> wr.bs_shift));
+    };
+    // activations: chunk c of a stage is k-part c / (16 MP), token (c / 16) % MP, 16-byte
+    // column c % 16; super-steps past K read the next row's bytes or zero (never used)
+    const int64_t mrows = a.M < MP ? a.M : MP;
+    const rsrc_t xr = make_rsrc(a.act, ((mrows - 1) * a.ld_act + a.act_cols) * 2);
+    const int ldb = static_cast<int>(a.ld_act) * 2;
+    u32x4_t xs[CH];
+    auto xload = [&](int rd) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + i * NT;
+            if (XCH % NT != 0 && c >= XCH) continue;
+            const int kq = c / (MP * 16), t = (c >> 4) % MP, kc = c & 15;
+            xs[i] = bload16(xr, t * ldb + (kq * per + rd) * XROW + kc * 16);
+        }
+    };
+    auto xstore = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + i * NT;
+            if (XCH % NT != 0 && c >= XCH) continue;
+            const int kq = c / (MP * 16), t = (c >> 4) % MP, kc = c & 15;
+            *reinterpret_cast<u32x4_t *>(s_x + b * XSTG + (kq * MP + t) * XROW +
+                                         ((kc ^ (t & 15)) << 4)) = xs[i];
+        }
+    };
+
+    float4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    const LoraDev &lo = a.lora[seg];
+    if (lo.has && kp == 0) {
+        for (int k0 = 0; k0 < lo.rank; k0 += 32) {
+            const int lim = lo.rank - (k0 + 8 * g);
+            const u32x4_t fa = (row < w.rows && lim > 0) ? gather8(lo.b + row * lo.rank + k0 + 8 * g, 1, lim)
+                                                         : (u32x4_t){0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int64_t m = 16 * mt + r;
+                const u32x4_t fb = (m < a.M && lim > 0) ? gather8(lo.t + m * lo.rank + k0 + 8 * g, 1, lim)
+                                                        : (u32x4_t){0u, 0u, 0u, 0u};
+                acc[mt] = mfma16<DT>(fa, fb, acc[mt]);
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] *= lo.scale;
+    }
+
+    WStage wst[WS];
+#pragma unroll
+    for (int b = 0; b < WS; ++b) wload(wst[b], b);
+    xload(0);
+    xstore(0);
+    __syncthreads();  // code2 table, activation stage 0
+
+    auto compute = [&](const WStage &s, int b) {
+        const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, s.abs, s_code2));
+        const uint8_t *xb = s_x + b * XSTG + kp * MP * XROW;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint32_t wd = ks == 0 ? s.raw.x : ks == 1 ? s.raw.y : ks == 2 ? s.raw.z : s.raw.w;
+            const u32x4_t fa = lookup8(tb, wd);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int t = 16 * mt + r;
+                const u32x4_t fb = *reinterpret_cast<const u32x4_t *>(
+                    xb + t * XROW + (((4 * g + ks) ^ (t & 15)) << 4));
+                acc[mt] = mfma16<DT>(fa, fb, acc[mt]);
+            }
+        }
+    };
+    // round rd: activations in stage rd & 1 (landed before the previous barrier); the next
+    // round's go to registers first and to the other stage after this round's arithmetic
+    auto round = [&](WStage &s, int rd) {
+        if (rd + 1 < per) xload(rd + 1);
+        if (rd < my_n) compute(s, rd & 1);
+        wload(s, rd + WS);
+        if (rd + 1 < per) xstore((rd + 1) & 1);
+        __syncthreads();
+    };
+    int rd = 0;
+    for (; rd + WS <= per; rd += WS) {
+#pragma unroll
+        for (int b = 0; b < WS; ++b) round(wst[b], rd + b);
+    }
+#pragma unroll
+    for (int b = 0; b < WS - 1; ++b)
+        if (rd + b < per) round(wst[b], rd + b);
+
+    if constexpr (KP > 1) {
+        float4_t *red = reinterpret_cast<float4_t *>(s_x);  // the stages are free now
+        if (kp > 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) red[(((kp - 1) * RT + rt) * MT + mt) * 64 + lane] = acc[mt];
+        }
+        __syncthreads();
+        if (kp == 0) {
+#pragma unroll
+            for (int q = 1; q < KP; ++q)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) acc[mt] += red[(((q - 1) * RT + rt) * MT + mt) * 64 + lane];
+        }
+    }
+    if (kp == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            epilogue16<DT>(a, acc[mt], p0 + 16 * rt + 4 * g, w.rows, a.seg_off[seg], 16 * mt + r);
+    }
+}
+
 // ------------------------------------------------------------------- small-M forward path
 //
 // Y = X W^T for M <= 32 * MT tokens (the decode regime; the planner launches MT = 1 only, the
@@ -2255,7 +2431,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial,
 struct Plan {
     int cfg;       // 0: 256x256 tile / 8 waves, 1: 128x128 tile / 4 waves, 3: 128x128 tile /
                    // two k-groups of 4 waves, 2: small-M path,
-                   // 4: decode path (M <= 16)
+                   // 4: decode path (M <= 16), 6: row streaming (M <= 2), 7: skinny path
+                   // (2 < M <= 64)
     int bp, bm;
     int splits;    // reduction splits of the tail tiles
     int64_t tiles;
@@ -2497,10 +2674,67 @@ bool rows_ok(int64_t m, const nf4_weight *ws, int nw) {
     return true;
 }
 
+// Skinny path (2 < M <= 64, K a multiple of 128): MT = 16-token groups and the workgroup shape
+// RT row tiles x KP k-parts (8 waves) from a cost model calibrated on the box (Qwen2.5-1.5B and
+// -7B projections at M = 8 .. 64, every shape timed):
+//   t = 5.35 us + 0.0377 us per 1000 weight elements of the busiest CU (ceil(workgroups / CUs)
+//       x 16 RT x K) + 0.0058 us per 1000 of them for each 16-token group past the first
+//       + 0.07 us per MB of activations the workgroups read (each reads all of X once);
+// the activation stages (2 KP MT x 8 KB) must fit in LDS and a k-part hold two super-steps.
+// Plan::bp holds the rows per workgroup (16 RT), Plan::waves KP, Plan::bm 16 MT; the cost (us)
+// is returned through `cost`.
+Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr) {
+    const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    const int64_t K = ws[0].cols, ss = K / DK;
+    static constexpr int kShapes[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
+    Plan best{};
+    double best_t = 1e30;
+    for (const auto &sh : kShapes) {
+        const int rt = sh[0], kp = sh[1];
+        if (kp * mt > 16 || (kp > 1 && ss < 2 * kp)) continue;
+        int64_t wgs = 0;
+        for (int i = 0; i < nw; ++i) wgs += (ws[i].rows + 16 * rt - 1) / (16 * rt);
+        const double busiest = double((wgs + kCUs - 1) / kCUs) * 16.0 * rt * double(K) / 1000.0;
+        const double x_mb = double(wgs) * double(m) * double(K) * 2.0 / 1e6;
+        const double t = 5.35 + busiest * (0.0377 + 0.0058 * (mt - 1)) + 0.07 * x_mb;
+        if (t < best_t) {
+            best = Plan{7, 16 * rt, 16 * mt, 1, wgs, kp, wgs};
+            best_t = t;
+        }
+    }
+    if (cost) *cost = best_t;
+    return best;
+}
+
+// The decode kernel's time by the same calibration (one workgroup per 16 rows, K split over
+// its waves): 4.26 us + 0.0637 us per 1000 elements of the busiest CU (+ 0.018 above 8 tokens).
+double decode_cost(int64_t m, const nf4_weight *ws, int nw) {
+    int64_t t16 = 0;
+    for (int i = 0; i < nw; ++i) t16 += (ws[i].rows + 15) / 16;
+    const double busiest = double((t16 + kCUs - 1) / kCUs) * 16.0 * double(ws[0].cols) / 1000.0;
+    return 4.26 + busiest * (m <= 8 ? 0.0637 : 0.0818);
+}
+
+// The skinny path takes 2 < M <= 64 with K a multiple of 128, except reductions longer than
+// twice the rows (down projections): there a workgroup per row tile leaves most CUs idle, and
+// the decode kernel (M <= 16, K split over its waves) or split-K tiles measured faster; at
+// M <= 16 it also has to beat the decode kernel's modelled time.
+bool skinny_ok(int64_t m, const nf4_weight *ws, int nw) {
+    if (m <= 2 || m > kSkinnyMaxM || ws[0].cols % DK != 0) return false;
+    int64_t rows = 0;
+    for (int i = 0; i < nw; ++i) rows += ws[i].rows;
+    if (ws[0].cols > 2 * rows) return false;
+    if (m > kDecodeMaxM) return true;
+    double t = 0;
+    plan_skinny(m, ws, nw, &t);
+    return t < decode_cost(m, ws, nw);
+}
+
 // rows_allowed: the row-streaming path's operand alignment holds (LoRA T and B read as dwords).
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1,
               bool rows_allowed = true) {
     if (tile < 0 && rows_allowed && rows_ok(m, ws, nw)) return plan_rows(m, ws, nw);
+    if (tile < 0 && skinny_ok(m, ws, nw)) return plan_skinny(m, ws, nw);
     if (tile < 0 && m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
     if (tile < 0 && m <= kGemvMaxM) return plan_gemv(m, ws, nw);
     int64_t big = 0, small = 0;
@@ -2525,10 +2759,24 @@ Plan plan_dx(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits 
     return make_plan(m, big, small, steps, kMaxSplits, K, ws_cap);
 }
 
+template <int DT, int MT>
+void launch_skinny(const GemmArgs &g, const Plan &p, hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(p.tiles)), block(512);
+    const int rt = p.bp / 16;
+    if (rt == 8) hipLaunchKernelGGL((skinny_kernel<DT, MT, 8, 1>), grid, block, 0, st, g);
+    else if (rt == 4) hipLaunchKernelGGL((skinny_kernel<DT, MT, 4, 2>), grid, block, 0, st, g);
+    else if (rt == 2) hipLaunchKernelGGL((skinny_kernel<DT, MT, 2, 4>), grid, block, 0, st, g);
+    else if constexpr (MT <= 2) hipLaunchKernelGGL((skinny_kernel<DT, MT, 1, 8>), grid, block, 0, st, g);
+}
+
 template <int DT>
 int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
-    if (p.cfg == 4) {
+    if (p.cfg == 7) {
+        if (p.bm == 16) launch_skinny<DT, 1>(g, p, st);
+        else if (p.bm == 32) launch_skinny<DT, 2>(g, p, st);
+        else launch_skinny<DT, 4>(g, p, st);
+    } else if (p.cfg == 4) {
         const dim3 block(p.waves * 64);
         if (p.waves == 8) hipLaunchKernelGGL((decode_kernel<DT, 8>), grid, block, 0, st, g);
         else if (p.waves == 4) hipLaunchKernelGGL((decode_kernel<DT, 4>), grid, block, 0, st, g);

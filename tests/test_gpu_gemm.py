@@ -81,6 +81,27 @@ def test_decode_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [5, 24, 40, 64])
+@pytest.mark.parametrize("shape", [(300, 256), (48, 1536), (40, 3584)])
+def test_skinny_dequant_is_bit_exact(cuda, m, shape, dtype):
+    """The skinny path (2 < M <= 64): m one-hot activation rows X = I[c0:c0+m] give the weight
+    columns c0 .. c0+m-1 exactly, for every column block: one to four 16-token groups, a token
+    group only partly used, and the workgroup shapes its planner picks by row count and K
+    (k-parts of 2 to 28 super-steps, partial last part; rows past a row tile)."""
+    from solution import kernels
+
+    n, k = shape
+    banner("skinny dequant exact", shape, m, dtype)
+    p, qs = random_weight(n, k, seed=n + 7 * k, dev=cuda)
+    ref = oracle_w16(p, qs, "bf16" if dtype == torch.bfloat16 else "f16").view(torch.int16)
+    eye = torch.eye(k, dtype=dtype, device=cuda)
+    for c0 in range(0, k, m):
+        c0 = min(c0, k - m)  # every block m rows (one or two rows would take the M <= 2 path)
+        y = kernels.linear_fwd(eye[c0:c0 + m], [(p, qs)])
+        assert torch.equal(y.t().contiguous().cpu().view(torch.int16), ref[:, c0:c0 + m]), c0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("proj", list(QWEN_15B))
 def test_qwen_projection_m2048(cuda, proj, dtype):
     from solution import kernels
@@ -215,7 +236,7 @@ def test_bias_grad_shapes(cuda, m, n, pad, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("m", [1, 8, 33, 64])
+@pytest.mark.parametrize("m", [1, 3, 8, 16, 17, 33, 48, 64])
 def test_small_m_stacked_bias_lora(cuda, m, dtype):
     """The small-M forward path (decode regime): stacked segments whose row counts are not
     multiples of its 32-row tiles, bias, LoRA on two segments; and a long reduction (split over
