@@ -69,6 +69,11 @@ def parse():
                     help="skip the int8 MLP input-gradient leg (the reference's T4 backward)")
     ap.add_argument("--no-norm-rope", action="store_true",
                     help="skip the RMSNorm / RoPE neighbours of the projection")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the small-M forward sweeps (gemv_15b, gemv_7b), printed as one "
+                         "JSON object: the command the decode-regime profiles are taken with")
+    ap.add_argument("--gemv-ms", default="1,8,64",
+                    help="token counts M of the small-M sweeps (comma-separated)")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times: the "
@@ -321,7 +326,7 @@ def norm_rope_leg(dtype, dev, reps=20):
 
 # -------------------------------------------------------------------- varlen stack (config 3)
 
-def varlen_stack_leg(dtype, dev, steps=5, warmup=2, gemv=True):
+def varlen_stack_leg(dtype, dev, steps=5, warmup=2, gemv=True, gemv_ms=(1, 8, 64)):
     """the 28-layer Qwen2.5-1.5B projection stack (7 NF4 weights per layer,
     seeds 1000 + 7 l + i) forward and backward on an unpadded batch of 4 sequences with lengths
     drawn uniformly from [64, 512] (seed 5), concatenated through cu_seqlens."""
@@ -345,7 +350,7 @@ def varlen_stack_leg(dtype, dev, steps=5, warmup=2, gemv=True):
         "gflop_per_step": round(fl / 1e9, 2), "tflops": round(tf, 2),
         "frac": round(tf / PEAK_MFMA_TFLOPS, 4), "steps": steps}}
     if gemv:
-        out["gemv_15b"] = gemv_sweep(st, torch, "28-layer Qwen2.5-1.5B stack, fp16")
+        out["gemv_15b"] = gemv_sweep(st, torch, "28-layer Qwen2.5-1.5B stack, fp16", gemv_ms)
     del st
     torch.cuda.empty_cache()
     return out
@@ -353,7 +358,7 @@ def varlen_stack_leg(dtype, dev, steps=5, warmup=2, gemv=True):
 
 # ------------------------------------------------------------ 7B bf16 and GEMV sweep (config 4)
 
-def qwen7b_legs(dev, steps=5, warmup=2, gemv=True, layers=28):
+def qwen7b_legs(dev, steps=5, warmup=2, gemv=True, layers=28, gemv_ms=(1, 8, 64)):
     """one Qwen2.5-7B layer (hidden 3584, intermediate 18944, kv 512) in
     bf16 at M = 8192, forward+backward; and the small-M dequant-GEMV regime (M in {1, 8, 64},
     forward) over the 28-layer 7B stack (3.3 GB of NF4 weights, far above the Infinity Cache),
@@ -381,9 +386,28 @@ def qwen7b_legs(dev, steps=5, warmup=2, gemv=True, layers=28):
         "tflops": round(tf, 2), "frac": round(tf / PEAK_MFMA_TFLOPS, 4),
         "gemm_us_per_launch": per}}
     if gemv:
-        out["gemv_7b"] = gemv_sweep(st, torch, "28-layer Qwen2.5-7B stack, bf16")
+        out["gemv_7b"] = gemv_sweep(st, torch, "28-layer Qwen2.5-7B stack, bf16", gemv_ms)
     del st
     torch.cuda.empty_cache()
+    return out
+
+
+def gemv_only(dev, ms_list):
+    """The two small-M sweeps alone, on stacks sized for the largest M (no M=2048 / 8192
+    buffers)."""
+    import torch
+
+    from solution.stack import QWEN2_7B, QWEN2_15B, ProjectionStack
+
+    out = {}
+    for leg, shape, dtype, seed, what in (
+            ("gemv_15b", QWEN2_15B, torch.float16, 1000, "28-layer Qwen2.5-1.5B stack, fp16"),
+            ("gemv_7b", QWEN2_7B, torch.bfloat16, 2000, "28-layer Qwen2.5-7B stack, bf16")):
+        st = ProjectionStack.synthetic(shape, 28, max(ms_list), dtype, dev, seed_base=seed,
+                                       seed_stride=7, rank=RANK, alpha=ALPHA)
+        out[leg] = gemv_sweep(st, torch, what, ms_list)
+        del st
+        torch.cuda.empty_cache()
     return out
 
 
@@ -729,6 +753,10 @@ def main():
 
     dev = torch.device("cuda:0")
     dtype = torch.float16 if args.dtype == "f16" else torch.bfloat16
+    gemv_ms = tuple(int(v) for v in args.gemv_ms.split(","))
+    if args.gemv_only:
+        print(json.dumps(gemv_only(dev, gemv_ms)), flush=True)
+        return
     wl = Workload(dtype, dev)
     names = ["fwd_qkv", "fwd_o", "fwd_gu", "fwd_down", "dx_down", "dx_gu", "dx_o", "dx_qkv"]
     for _ in range(args.warmup):
@@ -812,9 +840,9 @@ def main():
     if not args.no_norm_rope:
         out.update(norm_rope_leg(dtype, dev))
     if not args.no_stack:
-        out.update(varlen_stack_leg(dtype, dev, gemv=not args.no_gemv))
+        out.update(varlen_stack_leg(dtype, dev, gemv=not args.no_gemv, gemv_ms=gemv_ms))
     if not args.no_7b:
-        out.update(qwen7b_legs(dev, gemv=not args.no_gemv))
+        out.update(qwen7b_legs(dev, gemv=not args.no_gemv, gemv_ms=gemv_ms))
     for leg in ("gemv_15b", "gemv_7b"):  # weight streaming: bounded by the measured read rate
         for key, v in out.get(leg, {}).items():
             if isinstance(v, dict) and "gbps" in v:

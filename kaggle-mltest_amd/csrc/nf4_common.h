@@ -165,6 +165,23 @@ __device__ __forceinline__ u32x4_t lookup8(const Nf4Table &t, uint32_t p) {
     return (u32x4_t){o0, o1, o2, o3};
 }
 
+// The same 8 elements in nibble-plane order: the high nibbles' entries, then the low nibbles'
+// (elements 0, 2, 4, 6, 1, 3, 5, 7 as four packed pairs).  An MFMA reduction is indifferent to
+// the order of its k values as long as both operands use the same one: the other operand's 8
+// values go through `plane_order` once, which saves the two perms that restore element order.
+__device__ __forceinline__ u32x4_t lookup8_planes(const Nf4Table &t, uint32_t p) {
+    uint32_t o0, o1, o2, o3;
+    lookup4(t, (p >> 4) & 0x0F0F0F0Fu, o0, o1);
+    lookup4(t, p & 0x0F0F0F0Fu, o2, o3);
+    return (u32x4_t){o0, o1, o2, o3};
+}
+
+// 8 consecutive 16-bit values (x0 .. x7 as four packed pairs) in the order of lookup8_planes.
+__device__ __forceinline__ u32x4_t plane_order(u32x4_t c) {
+    return (u32x4_t){vperm(c.y, c.x, 0x05040100u), vperm(c.w, c.z, 0x05040100u),
+                     vperm(c.y, c.x, 0x07060302u), vperm(c.w, c.z, 0x07060302u)};
+}
+
 // The NF4 table of a weight in scalar registers (the same for every lane).
 __device__ __forceinline__ void load_code_sgpr(const float *code, float (&out)[16]) {
 #pragma unroll

@@ -1419,6 +1419,21 @@ __device__ __forceinline__ void epilogue16(const GemmArgs &a, const float4_t &ac
     }
 }
 
+// The fp32 partial sums of a split reduction, lane layout of epilogue16: partials
+// [splits][M][n_out] (tail_col0 = 0) for split_reduce_kernel, which adds the bias and rounds.
+__device__ __forceinline__ void partial16(const GemmArgs &a, const float4_t &acc, int64_t p,
+                                          int64_t p_end, int64_t col_off, int64_t m, int split) {
+    if (m >= a.M || p >= p_end) return;
+    float *dst = a.partial + (static_cast<int64_t>(split) * a.M + m) * a.tail_cols + col_off + p;
+    if (p + 4 <= p_end && ((a.tail_cols | col_off) & 3) == 0) {
+        *reinterpret_cast<float4_t *>(dst) = acc;
+    } else {
+        const float v[4] = {acc.x, acc.y, acc.z, acc.w};
+        for (int q = 0; q < 4; ++q)
+            if (p + q < p_end) dst[q] = v[q];
+    }
+}
+
 template <int DT, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerSimd)))
 void decode_kernel(const GemmArgs a) {
@@ -1540,48 +1555,62 @@ void decode_kernel(const GemmArgs a) {
 
 // ------------------------------------------------------------------ skinny forward path
 //
-// Y = X W^T for 2 < M <= 64 tokens (decode steps and small batches) with K a multiple of 128,
-// on v_mfma_f32_16x16x32: A = 16 weight rows dequantized straight into registers, B = 16
-// tokens.  A workgroup of RT x KP waves owns 16 RT weight rows of one segment: wave w takes the
-// 16-row tile w % RT and the k-part w / RT (KP contiguous ranges of 128-deep super-steps).
-// The activations, the one operand all of a workgroup's row tiles share, are read from memory
-// once per workgroup into LDS: in round r the stage holds, for each k-part kp, its super-step
-// kp * per + r for the 16 MT tokens ([KP][16 MT][128 k], two stages, loaded through registers
-// one round ahead by every thread, token rows >= M reading zero), and each wave reads its MT B
-// fragments per k-substep from there.  (One workgroup per 16 rows, each reading all of X from
-// L2, moved twice the weight bytes at M = 8.)  Lane l takes row 16 rt + l % 16 and the k values
-// 32 (l / 16) .. + 31 of a super-step (16 packed bytes, one absmax block); k-substep ks uses
-// 32 (l / 16) + 8 ks .. + 7, and the B fragment of token group mt the same k of token
-// 16 mt + l % 16 (LDS rows of 256 bytes, 16-byte chunk c of token t at c ^ (t % 16), so the 16
-// tokens of a fragment read hit 16 distinct bank groups).  A wave past the end of its k-part
-// (the last part may be shorter) skips the arithmetic of a round but keeps loading and meeting
-// the barriers.  The KP partial tiles are added in k-part order through LDS (deterministic).
+// Y = X W^T for 2 < M <= 64 tokens (decode steps and small batches) with K a multiple of the
+// super-step DKS (128 or 256), on v_mfma_f32_16x16x32: A = 16 weight rows dequantized straight
+// into registers, B = 16 tokens.  A workgroup of RT x KP waves owns 16 RT weight rows of one
+// segment: wave w takes the 16-row tile w % RT and the k-part w / RT (KP contiguous ranges of
+// DKS-deep super-steps).  The activations, the one operand all of a workgroup's row tiles
+// share, are read from memory once per workgroup into LDS: in round r the stage holds, for each
+// k-part kp, its super-step kp * per + r for the 16 MT tokens ([KP][16 MT][DKS k], two stages,
+// loaded through registers one round ahead by every thread, token rows >= M reading zero), and
+// each wave reads its MT B fragments per k-substep from there.  (One workgroup per 16 rows,
+// each reading all of X from L2, moved twice the weight bytes at M = 8.)  Lane l takes row
+// 16 rt + l % 16 and the k values DKS / 4 * (l / 16) .. + DKS / 4 - 1 of a super-step (DKS / 8
+// packed bytes inside one absmax block: blocks are at least 64 wide, so one table per lane and
+// super-step); k-substep ks uses the 8 values from DKS / 4 * (l / 16) + 8 ks, A in nibble-plane
+// order (lookup8_planes) and B, the same k of token 16 mt + l % 16, stored in that order in LDS
+// (plane_order when staged; rows of 2 DKS bytes, 16-byte chunk c of token t at c ^ (t % 16), so
+// the 16 tokens of a fragment read hit 16 distinct bank groups).  A wave past the end of its
+// k-part (the last part may be shorter) skips the arithmetic of a round but keeps loading and
+// meeting the barriers.  The KP partial tiles are added in k-part order through LDS
+// (deterministic).  DKS = 256 halves the tables, the barriers and the rounds of DKS = 128 and
+// doubles the weight bytes in flight; its stages need twice the LDS.
 constexpr int64_t kSkinnyMaxM = 64;
 
-template <int DT, int MT, int RT, int KP>
+template <int DT, int MT, int RT, int KP, int DKS>
 __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) {
     constexpr int NW = RT * KP, NT = NW * 64, MP = 16 * MT;
     constexpr int WS = 3;                 // weight register stages
-    constexpr int XROW = DK * 2;          // LDS bytes of one token's super-step
+    constexpr int NSUB = DKS / 32;        // k-substeps of a super-step
+    constexpr int XROW = DKS * 2;         // LDS bytes of one token's super-step
+    constexpr int CPT = DKS / 8;          // its 16-byte chunks
     constexpr int XSTG = KP * MP * XROW;  // one activation stage
     constexpr int XCH = XSTG / 16;        // its 16-byte chunks
     constexpr int CH = (XCH + NT - 1) / NT;
+    static_assert(DKS == 128 || DKS == 256, "super-steps of 128 or 256");
     static_assert(2 * XSTG + 1024 <= 160 * 1024, "two activation stages fit in LDS");
     static_assert((KP - 1) * RT * MT * 64 * 16 <= 2 * XSTG, "the k-part sums fit in the stages");
     __shared__ __attribute__((aligned(16))) uint8_t s_x[2 * XSTG];
     __shared__ float s_code2[256];
 
-    const int64_t tile = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(blockIdx.x));
+    // workgroup b: row tile b / splits, reduction split b % splits (super-steps
+    // [split * per_split, + per_split) of K)
+    const int nsplit = a.splits;
+    const int bid = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x));
+    const int64_t tile = bid / nsplit;
+    const int split = bid - static_cast<int>(tile) * nsplit;
     const int seg = seg_of_tile(a, a.map[0], tile);
     const int64_t p0 = uniform64((tile - a.map[0].tile_start[seg]) * (16 * RT));
     const DevWeight w = a.w[seg];
     const int64_t K = a.K;
-    const int ss = static_cast<int>(K / DK);
-    const int per = (ss + KP - 1) / KP;
+    const int ss = static_cast<int>(K / DKS);
+    const int s0 = split * static_cast<int>(a.per_split);
+    const int s1 = s0 + static_cast<int>(a.per_split) < ss ? s0 + static_cast<int>(a.per_split) : ss;
+    const int per = (s1 - s0 + KP - 1) / KP;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int rt = wave % RT, kp = wave / RT;
-    const int my0 = kp * per;
-    const int my_n = ss - my0 < per ? (ss - my0 > 0 ? ss - my0 : 0) : per;
+    const int my0 = s0 + kp * per;
+    const int my_n = s1 - my0 < per ? (s1 - my0 > 0 ? s1 - my0 : 0) : per;
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
 
@@ -1589,24 +1618,25 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
     float code_r[16];
     load_code_sgpr(w.code, code_r);
 
-    // weights: 16 packed bytes of this lane's row per super-step; a wave's loads past its part
-    // repeat its last super-step (cached bytes, never used)
+    // weights: DKS / 8 packed bytes of this lane's row per super-step; a wave's loads past its
+    // part repeat its last super-step (cached bytes, never used)
     const WeightRsrc wr = weight_rsrc(w);
     const int64_t row = p0 + 16 * rt + r;
-    const int wpk = static_cast<int>(row * (K >> 1) + 16 * g);
+    const int wpk = static_cast<int>(row * (K >> 1) + (DKS / 8) * g);
     const int wblk = static_cast<int>(row * (K >> wr.bs_shift));
     const int last = my_n > 0 ? my0 + my_n - 1 : 0;
     struct WStage {
-        u32x4_t raw;
+        u32x4_t raw[NSUB / 4];
         AbsIn abs;
     };
     auto wload = [&](WStage &s, int v) {
         const int st = my0 + v < last ? my0 + v : last;
-        s.raw = bload16(wr.packed, wpk + st * (DK / 2));
-        s.abs = absmax_bload(wr, wblk + ((st * DK + 32 * g) >> wr.bs_shift));
+#pragma unroll
+        for (int q = 0; q < NSUB / 4; ++q) s.raw[q] = bload16(wr.packed, wpk + st * (DKS / 2) + 16 * q);
+        s.abs = absmax_bload(wr, wblk + ((st * DKS + (DKS / 4) * g) >> wr.bs_shift));
     };
-    // activations: chunk c of a stage is k-part c / (16 MP), token (c / 16) % MP, 16-byte
-    // column c % 16; super-steps past K read the next row's bytes or zero (never used)
+    // activations: chunk c of a stage is k-part c / (CPT MP), token (c / CPT) % MP, 16-byte
+    // column c % CPT; super-steps past K read the next row's bytes or zero (never used)
     const int64_t mrows = a.M < MP ? a.M : MP;
     const rsrc_t xr = make_rsrc(a.act, ((mrows - 1) * a.ld_act + a.act_cols) * 2);
     const int ldb = static_cast<int>(a.ld_act) * 2;
@@ -1616,8 +1646,8 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
         for (int i = 0; i < CH; ++i) {
             const int c = static_cast<int>(threadIdx.x) + i * NT;
             if (XCH % NT != 0 && c >= XCH) continue;
-            const int kq = c / (MP * 16), t = (c >> 4) % MP, kc = c & 15;
-            xs[i] = bload16(xr, t * ldb + (kq * per + rd) * XROW + kc * 16);
+            const int kq = c / (MP * CPT), t = (c / CPT) % MP, kc = c % CPT;
+            xs[i] = bload16(xr, t * ldb + (s0 + kq * per + rd) * XROW + kc * 16);
         }
     };
     auto xstore = [&](int b) {
@@ -1625,9 +1655,9 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
         for (int i = 0; i < CH; ++i) {
             const int c = static_cast<int>(threadIdx.x) + i * NT;
             if (XCH % NT != 0 && c >= XCH) continue;
-            const int kq = c / (MP * 16), t = (c >> 4) % MP, kc = c & 15;
+            const int kq = c / (MP * CPT), t = (c / CPT) % MP, kc = c % CPT;
             *reinterpret_cast<u32x4_t *>(s_x + b * XSTG + (kq * MP + t) * XROW +
-                                         ((kc ^ (t & 15)) << 4)) = xs[i];
+                                         ((kc ^ (t & 15)) << 4)) = plane_order(xs[i]);
         }
     };
 
@@ -1635,7 +1665,7 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
     const LoraDev &lo = a.lora[seg];
-    if (lo.has && kp == 0) {
+    if (lo.has && kp == 0 && split == 0) {
         for (int k0 = 0; k0 < lo.rank; k0 += 32) {
             const int lim = lo.rank - (k0 + 8 * g);
             const u32x4_t fa = (row < w.rows && lim > 0) ? gather8(lo.b + row * lo.rank + k0 + 8 * g, 1, lim)
@@ -1663,14 +1693,15 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
         const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, s.abs, s_code2));
         const uint8_t *xb = s_x + b * XSTG + kp * MP * XROW;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const uint32_t wd = ks == 0 ? s.raw.x : ks == 1 ? s.raw.y : ks == 2 ? s.raw.z : s.raw.w;
-            const u32x4_t fa = lookup8(tb, wd);
+        for (int ks = 0; ks < NSUB; ++ks) {
+            const u32x4_t &raw = s.raw[ks / 4];
+            const uint32_t wd = ks % 4 == 0 ? raw.x : ks % 4 == 1 ? raw.y : ks % 4 == 2 ? raw.z : raw.w;
+            const u32x4_t fa = lookup8_planes(tb, wd);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int t = 16 * mt + r;
                 const u32x4_t fb = *reinterpret_cast<const u32x4_t *>(
-                    xb + t * XROW + (((4 * g + ks) ^ (t & 15)) << 4));
+                    xb + t * XROW + (((NSUB * g + ks) ^ (t & 15)) << 4));
                 acc[mt] = mfma16<DT>(fa, fb, acc[mt]);
             }
         }
@@ -1709,8 +1740,12 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
     }
     if (kp == 0) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-            epilogue16<DT>(a, acc[mt], p0 + 16 * rt + 4 * g, w.rows, a.seg_off[seg], 16 * mt + r);
+        for (int mt = 0; mt < MT; ++mt) {
+            if (nsplit > 1)
+                partial16(a, acc[mt], p0 + 16 * rt + 4 * g, w.rows, a.seg_off[seg], 16 * mt + r, split);
+            else
+                epilogue16<DT>(a, acc[mt], p0 + 16 * rt + 4 * g, w.rows, a.seg_off[seg], 16 * mt + r);
+        }
     }
 }
 
@@ -2443,6 +2478,7 @@ struct Plan {
     // tiles of tiling `cfg` (1 or 3); `tiles` then counts the second launch's tiles (estimate).
     int64_t head_ptiles;
     int rows_g = 0;  // row-streaming path: row groups per workgroup
+    int dks = 0;     // skinny path: super-step depth (128 or 256)
 
     int64_t blocks() const { return tail_start + (tiles - tail_start) * splits; }
 };
@@ -2674,32 +2710,59 @@ bool rows_ok(int64_t m, const nf4_weight *ws, int nw) {
     return true;
 }
 
-// Skinny path (2 < M <= 64, K a multiple of 128): MT = 16-token groups and the workgroup shape
-// RT row tiles x KP k-parts (8 waves) from a cost model calibrated on the box (Qwen2.5-1.5B and
-// -7B projections at M = 8 .. 64, every shape timed):
-//   t = 5.35 us + 0.0377 us per 1000 weight elements of the busiest CU (ceil(workgroups / CUs)
-//       x 16 RT x K) + 0.0058 us per 1000 of them for each 16-token group past the first
-//       + 0.07 us per MB of activations the workgroups read (each reads all of X once);
-// the activation stages (2 KP MT x 8 KB) must fit in LDS and a k-part hold two super-steps.
-// Plan::bp holds the rows per workgroup (16 RT), Plan::waves KP, Plan::bm 16 MT; the cost (us)
-// is returned through `cost`.
+// Skinny path (2 < M <= 64, K a multiple of 128): MT = 16-token groups, the workgroup shape
+// RT row tiles x KP k-parts (8 waves), the super-step DKS and the reduction splits S from a cost
+// model calibrated on the box (Qwen2.5-1.5B and -7B projections at M = 3 .. 64, 230 timed
+// shapes and splits; mean error 6 %):
+//   t = 3.99 us + 0.0416 us (DKS 128) or 0.0376 us (DKS 256) per 1000 weight elements the
+//       busiest CU holds, counting a k-part's idle super-steps (ceil(workgroups / CUs) x 16 RT
+//       x KP x ceil(K / DKS / S / KP) x DKS) + 0.0053 us per 1000 of them for each 16-token
+//       group past the first + 0.0725 us per MB of activations the workgroups read (each
+//       reads X over its part of K)
+//       + with S > 1: 3.56 us for the reduction launch + 0.315 us per MB of fp32 partials
+//       (8 S M N bytes: written, then read back).
+// DKS = 256 only for one token group: with more its longer-lived registers cost a workgroup
+// per CU (gate|up of Qwen2.5-7B at M = 24: 42 us against 36 us at DKS = 128).  The activation
+// stages (2 x KP x 16 MT tokens x DKS x 2 bytes) must fit in LDS and a k-part of a split hold
+// two super-steps.  Splits serve the long reductions over few rows (down projections), whose
+// row tiles alone leave most CUs idle.  Plan::bp holds the rows per workgroup (16 RT),
+// Plan::waves KP, Plan::bm 16 MT, Plan::dks DKS, Plan::splits S (tail_start 0: every tile
+// split); the cost (us) is returned through `cost`.
+constexpr bool skinny_fits(int kp, int mt, int dks) { return kp * mt * dks <= 2048; }
+
 Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr) {
     const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-    const int64_t K = ws[0].cols, ss = K / DK;
+    const int64_t K = ws[0].cols;
+    int64_t n_out = 0;
+    for (int i = 0; i < nw; ++i) n_out += ws[i].rows;
     static constexpr int kShapes[4][2] = {{8, 1}, {4, 2}, {2, 4}, {1, 8}};
     Plan best{};
     double best_t = 1e30;
-    for (const auto &sh : kShapes) {
-        const int rt = sh[0], kp = sh[1];
-        if (kp * mt > 16 || (kp > 1 && ss < 2 * kp)) continue;
-        int64_t wgs = 0;
-        for (int i = 0; i < nw; ++i) wgs += (ws[i].rows + 16 * rt - 1) / (16 * rt);
-        const double busiest = double((wgs + kCUs - 1) / kCUs) * 16.0 * rt * double(K) / 1000.0;
-        const double x_mb = double(wgs) * double(m) * double(K) * 2.0 / 1e6;
-        const double t = 5.35 + busiest * (0.0377 + 0.0058 * (mt - 1)) + 0.07 * x_mb;
-        if (t < best_t) {
-            best = Plan{7, 16 * rt, 16 * mt, 1, wgs, kp, wgs};
-            best_t = t;
+    for (const int dks : {256, 128}) {
+        if (K % dks != 0 || (dks == 256 && mt > 1)) continue;
+        const int64_t ss = K / dks;
+        const double per_elem = dks == 256 ? 0.0376 : 0.0416;
+        for (const auto &sh : kShapes) {
+            const int rt = sh[0], kp = sh[1];
+            if (!skinny_fits(kp, mt, dks)) continue;
+            int64_t wgs = 0;
+            for (int i = 0; i < nw; ++i) wgs += (ws[i].rows + 16 * rt - 1) / (16 * rt);
+            for (const int sp_try : {1, 2, 4, 8, 16}) {
+                const int64_t sps = (ss + sp_try - 1) / sp_try;  // super-steps per split
+                if (kp > 1 && sps < 2 * kp) break;
+                const int sp = static_cast<int>((ss + sps - 1) / sps);  // no empty last split
+                const int64_t per = (sps + kp - 1) / kp;
+                const double busy =
+                    double((wgs * sp + kCUs - 1) / kCUs) * 16.0 * rt * kp * per * dks / 1000.0;
+                const double x_mb = double(wgs) * double(m) * double(K) * 2.0 / 1e6;
+                double t = 3.99 + busy * (per_elem + 0.0053 * (mt - 1)) + 0.0725 * x_mb;
+                if (sp > 1) t += 3.56 + 0.315 * 8.0 * sp * double(m) * double(n_out) / 1e6;
+                if (t < best_t) {
+                    best = Plan{7, 16 * rt, 16 * mt, sp, wgs, kp, sp > 1 ? 0 : wgs};
+                    best.dks = dks;
+                    best_t = t;
+                }
+            }
         }
     }
     if (cost) *cost = best_t;
@@ -2715,19 +2778,14 @@ double decode_cost(int64_t m, const nf4_weight *ws, int nw) {
     return 4.26 + busiest * (m <= 8 ? 0.0637 : 0.0818);
 }
 
-// The skinny path takes 2 < M <= 64 with K a multiple of 128, except reductions longer than
-// twice the rows (down projections): there a workgroup per row tile leaves most CUs idle, and
-// the decode kernel (M <= 16, K split over its waves) or split-K tiles measured faster; at
-// M <= 16 it also has to beat the decode kernel's modelled time.
+// The skinny path takes 2 < M <= 64 with K a multiple of 128; at M <= 16 it also has to beat
+// the decode kernel's modelled time.
 bool skinny_ok(int64_t m, const nf4_weight *ws, int nw) {
     if (m <= 2 || m > kSkinnyMaxM || ws[0].cols % DK != 0) return false;
-    int64_t rows = 0;
-    for (int i = 0; i < nw; ++i) rows += ws[i].rows;
-    if (ws[0].cols > 2 * rows) return false;
-    if (m > kDecodeMaxM) return true;
     double t = 0;
     plan_skinny(m, ws, nw, &t);
-    return t < decode_cost(m, ws, nw);
+    if (t >= 1e29) return false;  // no workgroup shape fits
+    return m > kDecodeMaxM || t < decode_cost(m, ws, nw);
 }
 
 // rows_allowed: the row-streaming path's operand alignment holds (LoRA T and B read as dwords).
@@ -2759,23 +2817,51 @@ Plan plan_dx(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits 
     return make_plan(m, big, small, steps, kMaxSplits, K, ws_cap);
 }
 
+// false: no kernel of this shape (the planner never asks for one)
+template <int DT, int MT, int DKS>
+bool launch_skinny_d(const GemmArgs &g, int rt, dim3 grid, hipStream_t st) {
+    const dim3 block(512);
+    if (rt == 8) {
+        hipLaunchKernelGGL((skinny_kernel<DT, MT, 8, 1, DKS>), grid, block, 0, st, g);
+        return true;
+    }
+    if constexpr (skinny_fits(2, MT, DKS)) {
+        if (rt == 4) {
+            hipLaunchKernelGGL((skinny_kernel<DT, MT, 4, 2, DKS>), grid, block, 0, st, g);
+            return true;
+        }
+    }
+    if constexpr (skinny_fits(4, MT, DKS)) {
+        if (rt == 2) {
+            hipLaunchKernelGGL((skinny_kernel<DT, MT, 2, 4, DKS>), grid, block, 0, st, g);
+            return true;
+        }
+    }
+    if constexpr (skinny_fits(8, MT, DKS)) {
+        if (rt == 1) {
+            hipLaunchKernelGGL((skinny_kernel<DT, MT, 1, 8, DKS>), grid, block, 0, st, g);
+            return true;
+        }
+    }
+    return false;
+}
+
 template <int DT, int MT>
-void launch_skinny(const GemmArgs &g, const Plan &p, hipStream_t st) {
-    const dim3 grid(static_cast<unsigned>(p.tiles)), block(512);
-    const int rt = p.bp / 16;
-    if (rt == 8) hipLaunchKernelGGL((skinny_kernel<DT, MT, 8, 1>), grid, block, 0, st, g);
-    else if (rt == 4) hipLaunchKernelGGL((skinny_kernel<DT, MT, 4, 2>), grid, block, 0, st, g);
-    else if (rt == 2) hipLaunchKernelGGL((skinny_kernel<DT, MT, 2, 4>), grid, block, 0, st, g);
-    else if constexpr (MT <= 2) hipLaunchKernelGGL((skinny_kernel<DT, MT, 1, 8>), grid, block, 0, st, g);
+bool launch_skinny(const GemmArgs &g, const Plan &p, hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(p.blocks()));
+    if (p.dks == 256) return launch_skinny_d<DT, MT, 256>(g, p.bp / 16, grid, st);
+    if (p.dks == 128) return launch_skinny_d<DT, MT, 128>(g, p.bp / 16, grid, st);
+    return false;
 }
 
 template <int DT>
 int launch_fwd(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
     if (p.cfg == 7) {
-        if (p.bm == 16) launch_skinny<DT, 1>(g, p, st);
-        else if (p.bm == 32) launch_skinny<DT, 2>(g, p, st);
-        else launch_skinny<DT, 4>(g, p, st);
+        const bool ok = p.bm == 16 ? launch_skinny<DT, 1>(g, p, st)
+                        : p.bm == 32 ? launch_skinny<DT, 2>(g, p, st)
+                                     : launch_skinny<DT, 4>(g, p, st);
+        if (!ok) return NF4_ERR_UNSUPPORTED;
     } else if (p.cfg == 4) {
         const dim3 block(p.waves * 64);
         if (p.waves == 8) hipLaunchKernelGGL((decode_kernel<DT, 8>), grid, block, 0, st, g);
@@ -2985,7 +3071,9 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
         return status_of(hipGetLastError());
     }
     g.splits = p.splits;
-    g.per_split = (g.K / BR + p.splits - 1) / p.splits;
+    // reduction steps per split: BR-deep steps, or the skinny path's super-steps
+    const int64_t unit = p.cfg == 7 ? p.dks : BR;
+    g.per_split = (g.K / unit + p.splits - 1) / p.splits;
     const int64_t bp = p.bp, bm = p.bm;
     g.map[0].m_tiles = (m + bm - 1) / bm;
     g.map[0].tile_start[0] = 0;

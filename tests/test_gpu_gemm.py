@@ -80,24 +80,55 @@ def test_decode_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
         assert torch.equal(y.t().contiguous().cpu().view(torch.int16), ref[:, c0:c0 + 16]), c0
 
 
+# (segment rows, K, M, blocksize, nested): each case lands on one skinny workgroup shape by the
+# planner's cost model - token groups MT, row tiles RT, super-step DKS - noted per case
+SKINNY_CASES = [
+    ((1200,), 2048, 16, 64, True),        # MT 1, RT 1 (8 k-parts), DKS 128
+    ((5000,), 1024, 13, 64, True),        # MT 1, RT 2, DKS 128
+    ((5000,), 2048, 16, 128, False),      # MT 1, RT 2, DKS 256, block 128, fp32 absmax
+    ((9000,), 768, 16, 64, True),         # MT 1, RT 4, DKS 128
+    ((9000,), 1024, 16, 64, True),        # MT 1, RT 4, DKS 256
+    ((8960, 8960), 1536, 16, 64, True),   # MT 1, RT 8, DKS 256: gate|up of Qwen2.5-1.5B
+    ((8960, 8960), 1536, 3, 64, True),    # MT 1, RT 2, DKS 128: the same at 3 tokens
+    ((1200,), 2048, 24, 64, True),        # MT 2, RT 1
+    ((1200,), 1024, 17, 64, True),        # MT 2, RT 2
+    ((700, 500), 512, 24, 64, True),      # MT 2, RT 4, two segments
+    ((1200,), 256, 32, 64, True),         # MT 2, RT 8
+    ((1200,), 1024, 40, 64, True),        # MT 4, RT 2
+    ((1200,), 512, 64, 64, True),         # MT 4, RT 4
+    ((1200,), 256, 33, 64, True),         # MT 4, RT 8
+    ((1024,), 8192, 16, 64, True),        # MT 1, RT 2, 8 reduction splits (fp32 partials)
+    ((1024,), 8960, 24, 64, True),        # MT 2, RT 4, 14 splits
+    ((1024,), 4096, 40, 64, True),        # MT 4, RT 2, 4 splits
+    ((3584,), 18944, 8, 64, True),        # MT 1, RT 8, DKS 256, 8 splits, the last one shorter:
+                                          # down of Qwen2.5-7B
+]
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("m", [5, 24, 40, 64])
-@pytest.mark.parametrize("shape", [(300, 256), (48, 1536), (40, 3584)])
-def test_skinny_dequant_is_bit_exact(cuda, m, shape, dtype):
+@pytest.mark.parametrize("case", SKINNY_CASES, ids=lambda c: f"{'+'.join(map(str, c[0]))}x{c[1]}-m{c[2]}")
+def test_skinny_dequant_is_bit_exact(cuda, case, dtype):
     """The skinny path (2 < M <= 64): m one-hot activation rows X = I[c0:c0+m] give the weight
-    columns c0 .. c0+m-1 exactly, for every column block: one to four 16-token groups, a token
-    group only partly used, and the workgroup shapes its planner picks by row count and K
-    (k-parts of 2 to 28 super-steps, partial last part; rows past a row tile)."""
+    columns c0 .. c0+m-1 exactly (every stacked segment), over column blocks spread across K:
+    one to four 16-token groups, a token group only partly used, k-parts with a shorter last
+    part, rows past a row tile, and both super-step depths (their nibble-plane order of the
+    weight and activation fragments included)."""
     from solution import kernels
 
-    n, k = shape
-    banner("skinny dequant exact", shape, m, dtype)
-    p, qs = random_weight(n, k, seed=n + 7 * k, dev=cuda)
-    ref = oracle_w16(p, qs, "bf16" if dtype == torch.bfloat16 else "f16").view(torch.int16)
+    rows, k, m, bs, nested = case
+    banner("skinny dequant exact", rows, k, m, bs, nested, dtype)
+    ws, refs = [], []
+    for i, n in enumerate(rows):
+        p, qs = random_weight(n, k, seed=n + 7 * k + i, dev=cuda, blocksize=bs, nested=nested)
+        ws.append((p, qs))
+        refs.append(oracle_w16(p, qs, "bf16" if dtype == torch.bfloat16 else "f16").view(torch.int16))
+    ref = torch.cat(refs, 0)
     eye = torch.eye(k, dtype=dtype, device=cuda)
-    for c0 in range(0, k, m):
-        c0 = min(c0, k - m)  # every block m rows (one or two rows would take the M <= 2 path)
-        y = kernels.linear_fwd(eye[c0:c0 + m], [(p, qs)])
+    starts = sorted({min(c, k - m) for c in range(0, k, m)})
+    if len(starts) > 24:  # 24 blocks spread over K, the first and the last included
+        starts = [starts[round(i * (len(starts) - 1) / 23)] for i in range(24)]
+    for c0 in starts:
+        y = kernels.linear_fwd(eye[c0:c0 + m], ws)
         assert torch.equal(y.t().contiguous().cpu().view(torch.int16), ref[:, c0:c0 + m]), c0
 
 
@@ -260,11 +291,17 @@ def test_small_m_stacked_bias_lora(cuda, m, dtype):
     y = kernels.linear_fwd(x, segs, bias, loras)
     ref = o.linear_fwd(x, w, bias, [(0, 100, x, a0, b0, s), (136, 28, x, a2, b2, s)])
     assert_rel(y, ref, what="small-M stacked fwd")
-    # long K: 140 steps, split over workgroups
-    pd, qd = random_weight(96, 8960, seed=301, dev=cuda)
+    # long K, two segments, bias, LoRA on the second: the reduction split over workgroups
+    # (fp32 partials; the bias and the rounding in the fixed-order reduction kernel, the LoRA
+    # term in the first split's partial)
+    segs_d = [random_weight(n, 8960, seed=301 + n, dev=cuda) for n in (96, 40)]
+    wd = torch.cat([oracle_w16(p, q, dt) for p, q in segs_d])
     xd = _x(m, 8960, 34, cuda, dtype)
-    assert_rel(kernels.linear_fwd(xd, [(pd, qd)]), o.linear_fwd(xd, oracle_w16(pd, qd, dt)),
-               what="small-M long K")
+    bd = _x(1, 136, 35, cuda, dtype, std=0.5).view(-1)
+    ad = ((torch.rand(r, 8960, generator=g) * 2 - 1) / 8960 ** 0.5).to(dtype).to(cuda)
+    bbd = (torch.randn(40, r, generator=g) * 0.05).to(dtype).to(cuda)
+    yd = kernels.linear_fwd(xd, segs_d, bd, [kernels.make_lora(1, r, s, t=kernels.lora_xa(xd, ad), b=bbd)])
+    assert_rel(yd, o.linear_fwd(xd, wd, bd, [(96, 40, xd, ad, bbd, s)]), what="small-M long K")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
