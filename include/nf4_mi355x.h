@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define NF4_ABI_VERSION 3
+#define NF4_ABI_VERSION 4
 
 /* status codes */
 #define NF4_OK 0
@@ -64,14 +64,20 @@ typedef struct nf4_weight {
 
 /* A rank-r LoRA adapter on output segment `seg` of a stacked projection (peft semantics,
  * y_seg += scale * drop(x) @ A^T @ B^T; reference layer.py:875-878, 1072-1090).
- * Forward reads t and b; the input-gradient GEMM reads a and da. */
+ * Forward reads t and b.  With a == NULL, t holds drop(x) @ A^T (the caller's nf4_lora_xa).
+ * With a set (dropout off: drop(x) = x), the forward computes t = x @ A^T itself, rounded to
+ * the GEMM dtype as nf4_lora_xa rounds it, writes it to t (then a writable [M, rank] buffer:
+ * the backward pass needs it) and uses it; on the skinny small-M path (3 to 32 tokens, rank
+ * <= 16) inside the GEMM's own launch, else in a launch of its own before the GEMM.
+ * The input-gradient GEMM reads a and da. */
 typedef struct nf4_lora {
     int32_t seg;
     int32_t rank;          /* 1..64 */
     float scale;           /* alpha / r */
-    const void *t;         /* [M, rank] drop(x) @ A^T, GEMM dtype (forward) */
+    const void *t;         /* [M, rank] drop(x) @ A^T, GEMM dtype (forward; written if a) */
     const void *b;         /* [rows_seg, rank] LoRA B, GEMM dtype (forward) */
-    const void *a;         /* [rank, K] LoRA A, GEMM dtype (input gradient) */
+    const void *a;         /* [rank, K] LoRA A, GEMM dtype (input gradient; forward: see
+                            * above), 16-byte aligned in the forward */
     const void *da;        /* [M, rank] scale * dY_seg @ B, GEMM dtype (input gradient) */
 } nf4_lora;
 

@@ -56,6 +56,8 @@ struct LoraDev {
     const uint16_t *b;   // forward: [rows_seg, rank]
     const uint16_t *a;   // dx: [rank, K]
     const uint16_t *da;  // dx: [M, rank]
+    const uint16_t *xa;  // forward, computed in the launch: A [rank, K], and T = X A^T out to
+    uint16_t *t_out;     //   t_out [M, rank] (skinny path, rank <= 16); else null
     float scale;
     int rank;
     int has;
@@ -1577,21 +1579,26 @@ void decode_kernel(const GemmArgs a) {
 // doubles the weight bytes in flight; its stages need twice the LDS.
 constexpr int64_t kSkinnyMaxM = 64;
 
-template <int DT, int MT, int RT, int KP, int DKS>
+template <int DT, int MT, int RT, int KP, int DKS, bool FX>
 __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) {
     constexpr int NW = RT * KP, NT = NW * 64, MP = 16 * MT;
     constexpr int WS = 3;                 // weight register stages
     constexpr int NSUB = DKS / 32;        // k-substeps of a super-step
     constexpr int XROW = DKS * 2;         // LDS bytes of one token's super-step
     constexpr int CPT = DKS / 8;          // its 16-byte chunks
-    constexpr int XSTG = KP * MP * XROW;  // one activation stage
-    constexpr int XCH = XSTG / 16;        // its 16-byte chunks
+    constexpr int RS = MP + (FX ? 16 : 0);  // stage rows per k-part: tokens, then A's rows
+    constexpr int XSTG = KP * RS * XROW;  // one activation stage
+    constexpr int XCH = KP * MP * CPT;    // its 16-byte chunks of activations
     constexpr int CH = (XCH + NT - 1) / NT;
+    constexpr int ACH = KP * 16 * CPT;    // ... and of A's rows
+    constexpr int CHA = FX ? (ACH + NT - 1) / NT : 0;
     static_assert(DKS == 128 || DKS == 256, "super-steps of 128 or 256");
-    static_assert(2 * XSTG + 1024 <= 160 * 1024, "two activation stages fit in LDS");
-    static_assert((KP - 1) * RT * MT * 64 * 16 <= 2 * XSTG, "the k-part sums fit in the stages");
+    static_assert(2 * XSTG + 1024 + (FX ? MP * 32 : 0) <= 160 * 1024, "two stages fit in LDS");
+    static_assert(((KP - 1) * RT * MT + (FX ? (KP - 1) * MT : 0)) * 64 * 16 <= 2 * XSTG,
+                  "the k-part sums fit in the stages");
     __shared__ __attribute__((aligned(16))) uint8_t s_x[2 * XSTG];
     __shared__ float s_code2[256];
+    __shared__ __attribute__((aligned(16))) uint16_t s_t[FX ? MP : 1][16];  // T, token-major
 
     // workgroup b: row tile b / splits, reduction split b % splits (super-steps
     // [split * per_split, + per_split) of K)
@@ -1613,6 +1620,11 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
     const int my_n = s1 - my0 < per ? (s1 - my0 > 0 ? s1 - my0 : 0) : per;
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
+    const LoraDev &lo = a.lora[seg];
+    // the LoRA down-projection T = X A^T of this segment, computed here: A's rows ride in the
+    // activation stages and the first row tile's waves add its products (one per k-substep)
+    const bool fx = FX && lo.xa != nullptr;
+    const bool fx_wave = fx && rt == 0;
 
     for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = code2_entry(w, i);
     float code_r[16];
@@ -1641,6 +1653,9 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
     const rsrc_t xr = make_rsrc(a.act, ((mrows - 1) * a.ld_act + a.act_cols) * 2);
     const int ldb = static_cast<int>(a.ld_act) * 2;
     u32x4_t xs[CH];
+    u32x4_t xsa[CHA > 0 ? CHA : 1];
+    // A's rows (rank <= 16; rows past the rank read zero)
+    const rsrc_t ar = make_rsrc(lo.xa, fx ? int64_t(lo.rank) * K * 2 : 0);
     auto xload = [&](int rd) {
 #pragma unroll
         for (int i = 0; i < CH; ++i) {
@@ -1649,6 +1664,15 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
             const int kq = c / (MP * CPT), t = (c / CPT) % MP, kc = c % CPT;
             xs[i] = bload16(xr, t * ldb + (s0 + kq * per + rd) * XROW + kc * 16);
         }
+        if (fx) {
+#pragma unroll
+            for (int i = 0; i < CHA; ++i) {
+                const int c = static_cast<int>(threadIdx.x) + i * NT;
+                if (ACH % NT != 0 && c >= ACH) continue;
+                const int kq = c / (16 * CPT), j = (c / CPT) % 16, kc = c % CPT;
+                xsa[i] = bload16(ar, j * static_cast<int>(K * 2) + (s0 + kq * per + rd) * XROW + kc * 16);
+            }
+        }
     };
     auto xstore = [&](int b) {
 #pragma unroll
@@ -1656,16 +1680,27 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
             const int c = static_cast<int>(threadIdx.x) + i * NT;
             if (XCH % NT != 0 && c >= XCH) continue;
             const int kq = c / (MP * CPT), t = (c / CPT) % MP, kc = c % CPT;
-            *reinterpret_cast<u32x4_t *>(s_x + b * XSTG + (kq * MP + t) * XROW +
+            *reinterpret_cast<u32x4_t *>(s_x + b * XSTG + (kq * RS + t) * XROW +
                                          ((kc ^ (t & 15)) << 4)) = plane_order(xs[i]);
+        }
+        if (fx) {
+#pragma unroll
+            for (int i = 0; i < CHA; ++i) {
+                const int c = static_cast<int>(threadIdx.x) + i * NT;
+                if (ACH % NT != 0 && c >= ACH) continue;
+                const int kq = c / (16 * CPT), j = (c / CPT) % 16, kc = c % CPT;
+                *reinterpret_cast<u32x4_t *>(s_x + b * XSTG + (kq * RS + MP + j) * XROW +
+                                             ((kc ^ j) << 4)) = plane_order(xsa[i]);
+            }
         }
     };
 
-    float4_t acc[MT];
+    float4_t acc[MT], acc_t[FX ? MT : 1];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    const LoraDev &lo = a.lora[seg];
-    if (lo.has && kp == 0 && split == 0) {
+#pragma unroll
+    for (int mt = 0; mt < (FX ? MT : 1); ++mt) acc_t[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    if (lo.has && !fx && kp == 0 && split == 0) {
         for (int k0 = 0; k0 < lo.rank; k0 += 32) {
             const int lim = lo.rank - (k0 + 8 * g);
             const u32x4_t fa = (row < w.rows && lim > 0) ? gather8(lo.b + row * lo.rank + k0 + 8 * g, 1, lim)
@@ -1691,18 +1726,22 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
 
     auto compute = [&](const WStage &s, int b) {
         const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, s.abs, s_code2));
-        const uint8_t *xb = s_x + b * XSTG + kp * MP * XROW;
+        const uint8_t *xb = s_x + b * XSTG + kp * RS * XROW;
 #pragma unroll
         for (int ks = 0; ks < NSUB; ++ks) {
             const u32x4_t &raw = s.raw[ks / 4];
             const uint32_t wd = ks % 4 == 0 ? raw.x : ks % 4 == 1 ? raw.y : ks % 4 == 2 ? raw.z : raw.w;
             const u32x4_t fa = lookup8_planes(tb, wd);
+            u32x4_t fa_t = (u32x4_t){0u, 0u, 0u, 0u};
+            if (FX && fx_wave)
+                fa_t = *reinterpret_cast<const u32x4_t *>(xb + (MP + r) * XROW + (((NSUB * g + ks) ^ r) << 4));
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int t = 16 * mt + r;
                 const u32x4_t fb = *reinterpret_cast<const u32x4_t *>(
                     xb + t * XROW + (((NSUB * g + ks) ^ (t & 15)) << 4));
                 acc[mt] = mfma16<DT>(fa, fb, acc[mt]);
+                if (FX && fx_wave) acc_t[mt] = mfma16<DT>(fa_t, fb, acc_t[mt]);
             }
         }
     };
@@ -1726,9 +1765,14 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
 
     if constexpr (KP > 1) {
         float4_t *red = reinterpret_cast<float4_t *>(s_x);  // the stages are free now
+        float4_t *red_t = red + (KP - 1) * RT * MT * 64;
         if (kp > 0) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) red[(((kp - 1) * RT + rt) * MT + mt) * 64 + lane] = acc[mt];
+            if (FX && fx_wave) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) red_t[((kp - 1) * MT + mt) * 64 + lane] = acc_t[mt];
+            }
         }
         __syncthreads();
         if (kp == 0) {
@@ -1736,6 +1780,48 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
             for (int q = 1; q < KP; ++q)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) acc[mt] += red[(((q - 1) * RT + rt) * MT + mt) * 64 + lane];
+            if (FX && fx_wave) {
+#pragma unroll
+                for (int q = 1; q < KP; ++q)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc_t[mt] += red_t[((q - 1) * MT + mt) * 64 + lane];
+            }
+        }
+    }
+    if constexpr (FX) {
+        if (fx) {
+            // T rounded to the GEMM dtype (as the standalone down-projection writes it): ranks
+            // 4 g .. 4 g + 3 of token 16 mt + r in this lane; into LDS for the slab below, and
+            // out to t_out by the segment's first workgroup (the backward pass needs T)
+            if (fx_wave && kp == 0) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int t = 16 * mt + r;
+                    u32x2_t v;
+                    v.x = pack2<DT>(acc_t[mt].x, acc_t[mt].y);
+                    v.y = pack2<DT>(acc_t[mt].z, acc_t[mt].w);
+                    *reinterpret_cast<u32x2_t *>(&s_t[t][4 * g]) = v;
+                    if (p0 == 0 && t < a.M) {
+                        const uint16_t h[4] = {static_cast<uint16_t>(v.x), static_cast<uint16_t>(v.x >> 16),
+                                               static_cast<uint16_t>(v.y), static_cast<uint16_t>(v.y >> 16)};
+                        for (int q = 0; q < 4; ++q)
+                            if (4 * g + q < lo.rank) lo.t_out[t * lo.rank + 4 * g + q] = h[q];
+                    }
+                }
+            }
+            __syncthreads();
+            // the slab: Y_seg += scale * T B^T, k over the 16 (zero-padded) ranks
+            if (kp == 0) {
+                const int lim = lo.rank - 8 * g;
+                const u32x4_t fa = (row < w.rows && lim > 0) ? gather8(lo.b + row * lo.rank + 8 * g, 1, lim)
+                                                             : (u32x4_t){0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const u32x4_t fb = g < 2 ? *reinterpret_cast<const u32x4_t *>(&s_t[16 * mt + r][8 * g])
+                                             : (u32x4_t){0u, 0u, 0u, 0u};
+                    acc[mt] += mfma16<DT>(fa, fb, (float4_t){0.f, 0.f, 0.f, 0.f}) * lo.scale;
+                }
+            }
         }
     }
     if (kp == 0) {
@@ -2479,6 +2565,7 @@ struct Plan {
     int64_t head_ptiles;
     int rows_g = 0;  // row-streaming path: row groups per workgroup
     int dks = 0;     // skinny path: super-step depth (128 or 256)
+    int fx = 0;      // skinny path: LoRA down-projections computed in the launch
 
     int64_t blocks() const { return tail_start + (tiles - tail_start) * splits; }
 };
@@ -2778,21 +2865,40 @@ double decode_cost(int64_t m, const nf4_weight *ws, int nw) {
     return 4.26 + busiest * (m <= 8 ? 0.0637 : 0.0818);
 }
 
+// A skinny plan that can compute LoRA down-projections of rank <= 16 in its own launch: one
+// reduction split (T needs all of K), at most two token groups, and the stages hold 16 more
+// rows per k-part.
+bool skinny_fx_ok(const Plan &p, int xa_rank) {
+    const int mt = p.bm / 16;
+    return p.cfg == 7 && xa_rank >= 1 && xa_rank <= 16 && p.splits == 1 && mt <= 2 &&
+           skinny_fits(p.waves, mt + 1, p.dks);
+}
+
+// A standalone LoRA down-projection launch (nf4_lora_xa_multi, two adapters at decode token
+// counts), timed on the box: ~2.8 us + 1.1 ns per reduction element, and ~1.5 us between
+// launches.
+double xa_launch_cost(int64_t k) { return 4.3 + 0.00108 * double(k); }
+
 // The skinny path takes 2 < M <= 64 with K a multiple of 128; at M <= 16 it also has to beat
-// the decode kernel's modelled time.
-bool skinny_ok(int64_t m, const nf4_weight *ws, int nw) {
+// the decode kernel's modelled time, where a skinny plan that computes the LoRA
+// down-projections of the call (xa_rank > 0: rank of the largest) saves their own launch.
+bool skinny_ok(int64_t m, const nf4_weight *ws, int nw, int xa_rank) {
     if (m <= 2 || m > kSkinnyMaxM || ws[0].cols % DK != 0) return false;
     double t = 0;
-    plan_skinny(m, ws, nw, &t);
+    const Plan p = plan_skinny(m, ws, nw, &t);
     if (t >= 1e29) return false;  // no workgroup shape fits
-    return m > kDecodeMaxM || t < decode_cost(m, ws, nw);
+    if (m > kDecodeMaxM) return true;
+    const double saved = skinny_fx_ok(p, xa_rank) ? xa_launch_cost(ws[0].cols) : 0.0;
+    return t < decode_cost(m, ws, nw) + saved;
 }
 
 // rows_allowed: the row-streaming path's operand alignment holds (LoRA T and B read as dwords).
+// xa_rank: the call's LoRA adapters ask for their down-projections (rank of the largest), which
+// only moves the choice between the skinny and decode paths (neither needs a workspace).
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1,
-              bool rows_allowed = true) {
+              bool rows_allowed = true, int xa_rank = 0) {
     if (tile < 0 && rows_allowed && rows_ok(m, ws, nw)) return plan_rows(m, ws, nw);
-    if (tile < 0 && skinny_ok(m, ws, nw)) return plan_skinny(m, ws, nw);
+    if (tile < 0 && skinny_ok(m, ws, nw, xa_rank)) return plan_skinny(m, ws, nw);
     if (tile < 0 && m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
     if (tile < 0 && m <= kGemvMaxM) return plan_gemv(m, ws, nw);
     int64_t big = 0, small = 0;
@@ -2818,28 +2924,30 @@ Plan plan_dx(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits 
 }
 
 // false: no kernel of this shape (the planner never asks for one)
-template <int DT, int MT, int DKS>
+template <int DT, int MT, int DKS, bool FX>
 bool launch_skinny_d(const GemmArgs &g, int rt, dim3 grid, hipStream_t st) {
     const dim3 block(512);
-    if (rt == 8) {
-        hipLaunchKernelGGL((skinny_kernel<DT, MT, 8, 1, DKS>), grid, block, 0, st, g);
-        return true;
+    if constexpr (skinny_fits(1, MT + FX, DKS)) {
+        if (rt == 8) {
+            hipLaunchKernelGGL((skinny_kernel<DT, MT, 8, 1, DKS, FX>), grid, block, 0, st, g);
+            return true;
+        }
     }
-    if constexpr (skinny_fits(2, MT, DKS)) {
+    if constexpr (skinny_fits(2, MT + FX, DKS)) {
         if (rt == 4) {
-            hipLaunchKernelGGL((skinny_kernel<DT, MT, 4, 2, DKS>), grid, block, 0, st, g);
+            hipLaunchKernelGGL((skinny_kernel<DT, MT, 4, 2, DKS, FX>), grid, block, 0, st, g);
             return true;
         }
     }
-    if constexpr (skinny_fits(4, MT, DKS)) {
+    if constexpr (skinny_fits(4, MT + FX, DKS)) {
         if (rt == 2) {
-            hipLaunchKernelGGL((skinny_kernel<DT, MT, 2, 4, DKS>), grid, block, 0, st, g);
+            hipLaunchKernelGGL((skinny_kernel<DT, MT, 2, 4, DKS, FX>), grid, block, 0, st, g);
             return true;
         }
     }
-    if constexpr (skinny_fits(8, MT, DKS)) {
+    if constexpr (skinny_fits(8, MT + FX, DKS)) {
         if (rt == 1) {
-            hipLaunchKernelGGL((skinny_kernel<DT, MT, 1, 8, DKS>), grid, block, 0, st, g);
+            hipLaunchKernelGGL((skinny_kernel<DT, MT, 1, 8, DKS, FX>), grid, block, 0, st, g);
             return true;
         }
     }
@@ -2849,8 +2957,16 @@ bool launch_skinny_d(const GemmArgs &g, int rt, dim3 grid, hipStream_t st) {
 template <int DT, int MT>
 bool launch_skinny(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
-    if (p.dks == 256) return launch_skinny_d<DT, MT, 256>(g, p.bp / 16, grid, st);
-    if (p.dks == 128) return launch_skinny_d<DT, MT, 128>(g, p.bp / 16, grid, st);
+    if constexpr (MT <= 2) {
+        if (p.fx) {
+            if (p.dks == 256) return launch_skinny_d<DT, MT, 256, true>(g, p.bp / 16, grid, st);
+            if (p.dks == 128) return launch_skinny_d<DT, MT, 128, true>(g, p.bp / 16, grid, st);
+            return false;
+        }
+    }
+    if (p.fx) return false;
+    if (p.dks == 256) return launch_skinny_d<DT, MT, 256, false>(g, p.bp / 16, grid, st);
+    if (p.dks == 128) return launch_skinny_d<DT, MT, 128, false>(g, p.bp / 16, grid, st);
     return false;
 }
 
@@ -3017,9 +3133,11 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
     }
     if (ldy < n_out) return NF4_ERR_ARG;
     g.act_cols = g.K;
+    int xa_rank = 0;  // adapters whose down-projection T = x A^T this call computes
     for (int i = 0; i < nlora; ++i) {
         const nf4_lora &l = loras[i];
         if (l.seg < 0 || l.seg >= nw || l.rank < 1 || l.rank > 64 || !l.t || !l.b) return NF4_ERR_ARG;
+        if (l.a && !aligned(l.a, 16)) return NF4_ERR_ARG;
         LoraDev &d = g.lora[l.seg];
         if (d.has) return NF4_ERR_ARG;
         d.t = static_cast<const uint16_t *>(l.t);
@@ -3028,6 +3146,7 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
         d.scale = l.scale;
         d.has = 1;
         d.vec = l.rank % 8 == 0 && aligned(l.t, 16) && aligned(l.b, 16);
+        if (l.a) xa_rank = l.rank > xa_rank ? l.rank : xa_rank;
     }
     if (m == 0 || n_out == 0) return NF4_OK;
     g.bias = static_cast<const uint16_t *>(bias);
@@ -3043,8 +3162,39 @@ extern "C" int nf4_linear_fwd_tiled(const void *x, int64_t m, int64_t ldx, const
     bool lora_aligned = true;
     for (int i = 0; i < nlora; ++i)
         lora_aligned = lora_aligned && aligned(loras[i].b, 4) && aligned(loras[i].t, 4);
-    const Plan p = plan_fwd(m, ws, nw, tile, splits, lora_aligned);
+    Plan p = plan_fwd(m, ws, nw, tile, splits, lora_aligned, xa_rank);
     if (p.splits == 0) return NF4_ERR_ARG;
+    if (xa_rank > 0) {
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        p.fx = skinny_fx_ok(p, xa_rank);
+        nf4_lora_job jobs[kMaxSeg];
+        int nj = 0, rank0 = 0;
+        bool one_rank = true;
+        for (int i = 0; i < nlora; ++i) {
+            const nf4_lora &l = loras[i];
+            if (!l.a) continue;
+            if (p.fx) {  // the skinny kernel computes T itself and writes it to t
+                LoraDev &d = g.lora[l.seg];
+                d.xa = static_cast<const uint16_t *>(l.a);
+                d.t_out = static_cast<uint16_t *>(const_cast<void *>(l.t));
+            } else {     // a launch of their own first
+                jobs[nj++] = nf4_lora_job{x, ldx, g.K, l.a, const_cast<void *>(l.t), 1.0f, 0};
+                one_rank = one_rank && (rank0 == 0 || rank0 == l.rank);
+                rank0 = l.rank;
+            }
+        }
+        if (nj > 0 && one_rank && nj <= NF4_MAX_LORA_JOBS) {
+            st = nf4_lora_xa_multi(jobs, nj, m, rank0, dtype, s);
+            if (st != NF4_OK) return st;
+        } else {
+            for (int i = 0; i < nlora; ++i) {
+                const nf4_lora &l = loras[i];
+                if (!l.a || p.fx) continue;
+                st = nf4_lora_xa(x, m, g.K, ldx, l.a, l.rank, const_cast<void *>(l.t), dtype, s);
+                if (st != NF4_OK) return st;
+            }
+        }
+    }
     if (p.cfg == 6) {  // row streaming: row groups per segment, K parts per row
         g.splits = 1;
         g.rows_groups = p.rows_g;

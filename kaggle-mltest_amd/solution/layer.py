@@ -16,8 +16,10 @@ dropout output, which the reference's norm kernel writes (drop_q, drop_v; layer.
 and whose gradient its norm backward masks (layer.py:1072-1090, 135-164: dd_q = da_q A_q).
 The LoRA product is folded into the same GEMM launch as the weight product (one extra rank-r
 reduction slab), instead of the reference's separate mm's and fp32 add in the RoPE kernel; for
-an adapter on x the input-gradient term is folded into the dX GEMM the same way, while an
-adapter with its own input returns d(xd) unfolded (nf4_lora_ax_multi) for the norm backward.
+an adapter on x its down-projection t = x A^T is left to the projection call too (inside the
+GEMM launch on the small-M skinny path), and its input-gradient term is folded into the dX
+GEMM the same way, while an adapter with its own input gets t from its own launch and returns
+d(xd) unfolded (nf4_lora_ax_multi) for the norm backward.
 """
 
 from __future__ import annotations
@@ -172,10 +174,15 @@ class NF4Projection(torch.autograd.Function):
                 xd_dtypes.append(xd.dtype)
                 xin = _aligned_rows(xd.detach().to(dtype))
             t = torch.empty((x.shape[0], a16.shape[0]), dtype=dtype, device=x.device)
-            jobs.append((a16.shape[0], kernels.lora_job(xin, a16, t)))
-            structs.append(kernels.make_lora(ad.seg, a16.shape[0], ad.scale, t=t, b=b16))
+            if xd is None:  # t = x A^T: the projection's own call computes it
+                if a16.data_ptr() % 16:
+                    a16 = a16.clone()
+                structs.append(kernels.make_lora(ad.seg, a16.shape[0], ad.scale, t=t, b=b16, a=a16))
+            else:
+                jobs.append((a16.shape[0], kernels.lora_job(xin, a16, t)))
+                structs.append(kernels.make_lora(ad.seg, a16.shape[0], ad.scale, t=t, b=b16))
             saved += [t, a16, b16] + ([xin] if xd is not None else [])
-        _run_jobs(kernels.lora_xa_multi, jobs, x)  # t = xd A^T for every adapter
+        _run_jobs(kernels.lora_xa_multi, jobs, x)  # t = xd A^T for the adapters with own input
         b = None if bias is None else bias.detach().to(dtype).contiguous()
         y = kernels.linear_fwd(x, spec.weights, b, structs)
         ctx.spec = spec

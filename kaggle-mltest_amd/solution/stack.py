@@ -9,8 +9,10 @@ layer reads fixed input buffers, so a step is exactly the projection work of the
 
 Every launch goes through the C ABI with argument arrays built once, on torch's current
 stream, in the order the reference runs them:
-  forward, per layer:  t_q = X A_q^T and t_v = X A_v^T (one launch, kept per layer for the
-                       backward); q|k|v (+bias, +LoRA); o; gate|up; down
+  forward, per layer:  q|k|v (+bias, +LoRA, whose t_q = X A_q^T and t_v = X A_v^T the call
+                       computes and keeps per layer for the backward: inside the GEMM launch
+                       on the skinny small-M path, else one launch of its own before it); o;
+                       gate|up; down
   backward, reversed:  dX down; dX gate|up; dX o; da_q, da_v (one launch); dB_q, dB_v, dA_q,
                        dA_v (one launch); dX q|k|v (+LoRA)
 """
@@ -107,17 +109,16 @@ class ProjectionStack:
             f = lambda *s: torch.empty(s, dtype=torch.float32, device=self.dev)  # noqa: E731
             L["gb_q"], L["gb_v"], L["ga_q"], L["ga_v"] = f(h, rank), f(kv, rank), f(rank, h), f(rank, h)
             P, Lo = (lambda t: t.data_ptr()), _lib.NF4Lora
-            L["t_q"], L["t_v"] = e(mt, rank), e(mt, rank)  # t = X A^T, read again by dB
-            L["fwd_loras"] = (Lo * 2)(Lo(0, rank, self.scale, P(L["t_q"]), P(L["b_q"]), None, None),
-                                      Lo(2, rank, self.scale, P(L["t_v"]), P(L["b_v"]), None, None))
+            # t = X A^T, computed by the q|k|v forward itself (A given) and read again by dB
+            L["t_q"], L["t_v"] = e(mt, rank), e(mt, rank)
+            L["fwd_loras"] = (Lo * 2)(Lo(0, rank, self.scale, P(L["t_q"]), P(L["b_q"]), P(L["a_q"]), None),
+                                      Lo(2, rank, self.scale, P(L["t_v"]), P(L["b_v"]), P(L["a_v"]), None))
             L["dx_loras"] = (Lo * 2)(Lo(0, rank, self.scale, None, None, P(L["a_q"]), P(self.da_q)),
                                      Lo(2, rank, self.scale, None, None, P(L["a_v"]), P(self.da_v)))
             # the side products of both adapters, one launch each (nf4_lora_job arrays)
             J, es = _lib.NF4LoraJob, self.dy_qkv.element_size()
             dq, dv = P(self.dy_qkv), P(self.dy_qkv) + (h + kv) * es
             nq = self.n_qkv
-            L["xa_jobs"] = (J * 2)(J(P(self.x), h, h, P(L["a_q"]), P(L["t_q"]), 1.0, 0),
-                                   J(P(self.x), h, h, P(L["a_v"]), P(L["t_v"]), 1.0, 0))
             L["da_jobs"] = (J * 2)(J(dq, nq, h, P(L["b_q"]), P(self.da_q), self.scale, 0),
                                    J(dv, nq, kv, P(L["b_v"]), P(self.da_v), self.scale, 0))
             L["wg_jobs"] = (J * 4)(J(dq, nq, h, P(L["t_q"]), P(L["gb_q"]), self.scale, 0),
@@ -208,7 +209,6 @@ class ProjectionStack:
         ws = self.ws
         for li in (range(len(self.per_layer)) if layers is None else layers):
             L = self.per_layer[li]
-            self._chk(lib.nf4_lora_xa_multi(L["xa_jobs"], 2, m, r, dt, s), "xa")
             self._timed(ev, "fwd_qkv", lambda: lib.nf4_linear_fwd(
                 P(self.x), m, h, L["qkv"], 3, P(L["bias"]), L["fwd_loras"], 2, P(self.y_qkv), nq,
                 dt, P(ws["qkv"][0]), ws["qkv"][1], s))

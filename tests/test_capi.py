@@ -58,7 +58,7 @@ def test_struct_layouts_match_header():
 
 
 def test_version_and_status_strings(lib):
-    assert lib.nf4_abi_version() == 3
+    assert lib.nf4_abi_version() == 4
     assert lib.nf4_status_string(0) == b"ok"
     assert b"unsupported" in lib.nf4_status_string(2)
 

@@ -305,6 +305,46 @@ def test_small_m_stacked_bias_lora(cuda, m, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,r", [(1, 16), (3, 16), (8, 8), (8, 16), (16, 16), (17, 16), (32, 16),
+                                 (8, 32), (33, 16), (64, 16), (100, 16)])
+@pytest.mark.parametrize("shape", [((300, 64, 40), 640), ((1536, 256, 256), 1536)],
+                         ids=["300+64+40x640", "qkv-1.5B"])
+def test_forward_computes_lora_down_projection(cuda, shape, m, r, dtype):
+    """An adapter with `a` set in the forward: the call computes t = x A^T itself (inside the
+    skinny GEMM launch at 3 to 32 tokens with rank <= 16, ranks below 16 zero-padded; in a
+    launch of its own at other token counts, rank 32, or on other paths), writes it to t and
+    uses it.  t is nf4_lora_xa's up to a rounding step (the fp32 sums run in another order) and
+    Y matches the call given the caller's t, and the fp32 oracle."""
+    from solution import kernels
+
+    rows, k = shape
+    s = 2.0
+    banner("forward with LoRA down-projection", rows, k, m, r, dtype)
+    dt = "bf16" if dtype == torch.bfloat16 else "f16"
+    segs = [random_weight(n, k, seed=400 + n, dev=cuda) for n in rows]
+    w = torch.cat([oracle_w16(p, q, dt) for p, q in segs])
+    x = _x(m, k, 41, cuda, dtype)
+    bias = _x(1, sum(rows), 42, cuda, dtype, std=0.5).view(-1)
+    g = torch.Generator().manual_seed(43)
+    a0, a2 = [((torch.rand(r, k, generator=g) * 2 - 1) / k ** 0.5).to(dtype).to(cuda) for _ in range(2)]
+    b0 = (torch.randn(rows[0], r, generator=g) * 0.05).to(dtype).to(cuda)
+    b2 = (torch.randn(rows[2], r, generator=g) * 0.05).to(dtype).to(cuda)
+    t_ref = [kernels.lora_xa(x, a0), kernels.lora_xa(x, a2)]
+    y_given = kernels.linear_fwd(x, segs, bias, [kernels.make_lora(0, r, s, t=t_ref[0], b=b0),
+                                                 kernels.make_lora(2, r, s, t=t_ref[1], b=b2)])
+    t = [torch.full((m, r), float("nan"), dtype=dtype, device=cuda) for _ in range(2)]
+    y = kernels.linear_fwd(x, segs, bias, [kernels.make_lora(0, r, s, t=t[0], b=b0, a=a0),
+                                           kernels.make_lora(2, r, s, t=t[1], b=b2, a=a2)])
+    eps = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+    for got, ref in zip(t, t_ref):
+        scale = ref.float().abs().max().item()
+        torch.testing.assert_close(got.float(), ref.float(), rtol=2 * eps, atol=eps * scale)
+    assert_rel(y, y_given, what="forward with computed t vs given t")
+    ref = o.linear_fwd(x, w, bias, [(0, rows[0], x, a0, b0, s), (sum(rows[:2]), rows[2], x, a2, b2, s)])
+    assert_rel(y, ref, what="forward with computed t vs oracle")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m,k,r", [(1, 3584, 16), (2, 1536, 16), (5, 2056, 8), (8, 4096, 16),
                                    (9, 1536, 16)])
 def test_lora_xa_decode_sizes(cuda, dtype, m, k, r):
