@@ -130,6 +130,11 @@ int nf4_dequant_table(const void *dev_table, int nw, int64_t blocks, int out_dty
 /* Y[M, sum(rows)] = X[M, K] @ W_stack^T (+ bias) (+ sum over loras scale * T @ B^T on the
  * lora's segment columns), W dequantized inside the GEMM main loop, fp32 accumulation, one
  * rounding to dtype (F16 or BF16).  X rows are ldx elements apart, Y rows ldy.
+ * Weight: from 3 tokens on, each element is round(code * absmax) in dtype, the dequantized
+ * weight bit for bit.  At M <= 2 (the decode GEMV regime, where the reference defers to
+ * bitsandbytes' GEMV: fp32 code * fp32 absmax, nf4.py:15-16, 105-118) the product is
+ * round(code) * x in fp32, scaled per block by the fp32 absmax: bitsandbytes' arithmetic with
+ * the 16 codes rounded to dtype (relative error <= 2^-9 in bf16, 2^-12 in fp16 per code).
  * Replaces: F.linear(x, dequantize_nf4(W), bias) in NF4Linear.forward (nf4.py:84-91); the
  *           addmm / mm projection GEMMs of FusedDecoderLayer.forward with the LoRA terms
  *           (layer.py:871-878, 893, 914, 929); RecomputedMLP's forward GEMMs (mlp.py:47-54).

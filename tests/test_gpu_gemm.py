@@ -537,6 +537,37 @@ def test_rows_decode_one_hot_is_exact(cuda, m, shapes, bs, nested, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("shape", [(1536, 1536), (512, 3584), (256, 8960)])
+def test_rows_decode_against_fp32_code_product(cuda, m, shape, dtype):
+    """The row-streaming path (M <= 2) against the product bitsandbytes' decode GEMV forms, fp32
+    code x fp32 absmax x activation (the reference's small-M numerics, nf4.py:15-16, 105-118),
+    with the bound that follows from its one deviation: the 16 codes enter the GEMM rounded to
+    its dtype, a relative error of at most u = 2^-9 (bf16) or 2^-12 (fp16) per code, so for
+    every output n
+        |y - sum_k W32[n,k] x[k]| <= u sum_k |W32[n,k] x[k]| + 2u |y_ref| + 2^-20 sum_k |W32 x|
+    (code rounding, the final rounding to the dtype, fp32 accumulation).  Activations of mixed
+    sign and magnitude, K of one, two and five 1 KB slots."""
+    from solution import kernels
+    from tests.gpu_util import to_oracle_state
+
+    n, k = shape
+    banner("rows decode vs fp32-code product", m, shape, dtype)
+    p, qs = random_weight(n, k, seed=n + 5 * k, dev=cuda)
+    pn, st = to_oracle_state(p, qs)
+    w32 = torch.from_numpy(o.dequantize(pn, st, "f32")).double()  # fp32(code * absmax)
+    x = _x(m, k, 61, cuda, dtype)
+    y = kernels.linear_fwd(x, [(p, qs)]).double().cpu()
+    xd = x.double().cpu()
+    ref = xd @ w32.t()
+    mag = xd.abs() @ w32.abs().t()
+    u = 2.0 ** -9 if dtype == torch.bfloat16 else 2.0 ** -12
+    bound = u * mag + 2 * u * ref.abs() + 2.0 ** -20 * mag
+    err = (y - ref).abs()
+    assert bool((err <= bound).all()), f"max excess {(err - bound).max().item():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_rows_decode_qkv_bias_lora(cuda, m, dtype):
     """Stacked q|k|v with bias and LoRA on q and v at M <= 4 tokens (the row-streaming path up to
