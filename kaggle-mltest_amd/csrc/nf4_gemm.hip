@@ -2817,7 +2817,10 @@ bool rows_ok(int64_t m, const nf4_weight *ws, int nw) {
 // split); the cost (us) is returned through `cost`.
 constexpr bool skinny_fits(int kp, int mt, int dks) { return kp * mt * dks <= 2048; }
 
-Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr) {
+// fx_only: only plans that can compute a LoRA down-projection of rank <= 16 in the launch (one
+// split, the stages 16 rows taller).
+Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr,
+                 bool fx_only = false) {
     const int mt = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
     const int64_t K = ws[0].cols;
     int64_t n_out = 0;
@@ -2831,13 +2834,14 @@ Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr
         const double per_elem = dks == 256 ? 0.0376 : 0.0416;
         for (const auto &sh : kShapes) {
             const int rt = sh[0], kp = sh[1];
-            if (!skinny_fits(kp, mt, dks)) continue;
+            if (!skinny_fits(kp, mt + (fx_only ? 1 : 0), dks)) continue;
             int64_t wgs = 0;
             for (int i = 0; i < nw; ++i) wgs += (ws[i].rows + 16 * rt - 1) / (16 * rt);
             for (const int sp_try : {1, 2, 4, 8, 16}) {
                 const int64_t sps = (ss + sp_try - 1) / sp_try;  // super-steps per split
                 if (kp > 1 && sps < 2 * kp) break;
                 const int sp = static_cast<int>((ss + sps - 1) / sps);  // no empty last split
+                if (fx_only && (sp > 1 || mt > 2)) break;
                 const int64_t per = (sps + kp - 1) / kp;
                 const double busy =
                     double((wgs * sp + kCUs - 1) / kCUs) * 16.0 * rt * kp * per * dks / 1000.0;
@@ -2867,7 +2871,8 @@ double decode_cost(int64_t m, const nf4_weight *ws, int nw) {
 
 // A skinny plan that can compute LoRA down-projections of rank <= 16 in its own launch: one
 // reduction split (T needs all of K), at most two token groups, and the stages hold 16 more
-// rows per k-part.
+// rows per k-part.  (With four token groups the plans that fit, 1 or 2 k-parts, measured
+// slower than the best plan plus a separate launch: 7B q|k|v at M = 64 29.1 vs 26.6 us.)
 bool skinny_fx_ok(const Plan &p, int xa_rank) {
     const int mt = p.bm / 16;
     return p.cfg == 7 && xa_rank >= 1 && xa_rank <= 16 && p.splits == 1 && mt <= 2 &&
@@ -2878,18 +2883,39 @@ bool skinny_fx_ok(const Plan &p, int xa_rank) {
 // counts), timed on the box: ~2.8 us + 1.1 ns per reduction element, and ~1.5 us between
 // launches.
 double xa_launch_cost(int64_t k) { return 4.3 + 0.00108 * double(k); }
+constexpr double kFxCost = 2.0;
+
+// The skinny plan for the call: when it has LoRA down-projections to compute (xa_rank > 0: rank
+// of the largest), the best plan plus their own launch against the best plan that computes
+// them itself.  Either has no workspace when the plan without them has none, so the workspace
+// query, which does not see the adapters, stays valid.
+Plan choose_skinny(int64_t m, const nf4_weight *ws, int nw, int xa_rank, double *cost) {
+    double t = 0;
+    Plan p = plan_skinny(m, ws, nw, &t);
+    if (xa_rank > 0 && t < 1e29) {
+        // computing T in the launch adds ~2 us to it (7B q|k|v at M = 8: 12.8 vs 10.6 us)
+        t += skinny_fx_ok(p, xa_rank) ? kFxCost : xa_launch_cost(ws[0].cols);
+        double tf = 0;
+        const Plan pf = plan_skinny(m, ws, nw, &tf, true);
+        if (xa_rank <= 16 && tf + kFxCost < t) {
+            p = pf;
+            t = tf + kFxCost;
+        }
+    }
+    *cost = t;
+    return p;
+}
 
 // The skinny path takes 2 < M <= 64 with K a multiple of 128; at M <= 16 it also has to beat
-// the decode kernel's modelled time, where a skinny plan that computes the LoRA
-// down-projections of the call (xa_rank > 0: rank of the largest) saves their own launch.
+// the decode kernel's modelled time (plus the LoRA down-projections' own launch, which the
+// decode kernel never folds).
 bool skinny_ok(int64_t m, const nf4_weight *ws, int nw, int xa_rank) {
     if (m <= 2 || m > kSkinnyMaxM || ws[0].cols % DK != 0) return false;
     double t = 0;
-    const Plan p = plan_skinny(m, ws, nw, &t);
+    choose_skinny(m, ws, nw, xa_rank, &t);
     if (t >= 1e29) return false;  // no workgroup shape fits
     if (m > kDecodeMaxM) return true;
-    const double saved = skinny_fx_ok(p, xa_rank) ? xa_launch_cost(ws[0].cols) : 0.0;
-    return t < decode_cost(m, ws, nw) + saved;
+    return t < decode_cost(m, ws, nw) + (xa_rank > 0 ? xa_launch_cost(ws[0].cols) : 0.0);
 }
 
 // rows_allowed: the row-streaming path's operand alignment holds (LoRA T and B read as dwords).
@@ -2898,7 +2924,10 @@ bool skinny_ok(int64_t m, const nf4_weight *ws, int nw, int xa_rank) {
 Plan plan_fwd(int64_t m, const nf4_weight *ws, int nw, int tile = -1, int splits = 1,
               bool rows_allowed = true, int xa_rank = 0) {
     if (tile < 0 && rows_allowed && rows_ok(m, ws, nw)) return plan_rows(m, ws, nw);
-    if (tile < 0 && skinny_ok(m, ws, nw, xa_rank)) return plan_skinny(m, ws, nw);
+    if (tile < 0 && skinny_ok(m, ws, nw, xa_rank)) {
+        double t = 0;
+        return choose_skinny(m, ws, nw, xa_rank, &t);
+    }
     if (tile < 0 && m <= kDecodeMaxM && ws[0].cols % DK == 0) return plan_decode(ws, nw);
     if (tile < 0 && m <= kGemvMaxM) return plan_gemv(m, ws, nw);
     int64_t big = 0, small = 0;
@@ -2957,15 +2986,15 @@ bool launch_skinny_d(const GemmArgs &g, int rt, dim3 grid, hipStream_t st) {
 template <int DT, int MT>
 bool launch_skinny(const GemmArgs &g, const Plan &p, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(p.blocks()));
-    if constexpr (MT <= 2) {
-        if (p.fx) {
-            if (p.dks == 256) return launch_skinny_d<DT, MT, 256, true>(g, p.bp / 16, grid, st);
-            if (p.dks == 128) return launch_skinny_d<DT, MT, 128, true>(g, p.bp / 16, grid, st);
-            return false;
-        }
+    if constexpr (MT == 1) {  // the planner takes 256-deep super-steps for one token group only
+        if (p.dks == 256)
+            return p.fx ? launch_skinny_d<DT, MT, 256, true>(g, p.bp / 16, grid, st)
+                        : launch_skinny_d<DT, MT, 256, false>(g, p.bp / 16, grid, st);
+    }
+    if constexpr (MT <= 2) {  // T in the launch: at most two token groups
+        if (p.fx) return p.dks == 128 && launch_skinny_d<DT, MT, 128, true>(g, p.bp / 16, grid, st);
     }
     if (p.fx) return false;
-    if (p.dks == 256) return launch_skinny_d<DT, MT, 256, false>(g, p.bp / 16, grid, st);
     if (p.dks == 128) return launch_skinny_d<DT, MT, 128, false>(g, p.bp / 16, grid, st);
     return false;
 }
