@@ -2799,15 +2799,20 @@ bool rows_ok(int64_t m, const nf4_weight *ws, int nw) {
 
 // Skinny path (2 < M <= 64, K a multiple of 128): MT = 16-token groups, the workgroup shape
 // RT row tiles x KP k-parts (8 waves), the super-step DKS and the reduction splits S from a cost
-// model calibrated on the box (Qwen2.5-1.5B and -7B projections at M = 3 .. 64, 230 timed
-// shapes and splits; mean error 6 %):
-//   t = 3.99 us + 0.0416 us (DKS 128) or 0.0376 us (DKS 256) per 1000 weight elements the
-//       busiest CU holds, counting a k-part's idle super-steps (ceil(workgroups / CUs) x 16 RT
-//       x KP x ceil(K / DKS / S / KP) x DKS) + 0.0053 us per 1000 of them for each 16-token
-//       group past the first + 0.0725 us per MB of activations the workgroups read (each
-//       reads X over its part of K)
-//       + with S > 1: 3.56 us for the reduction launch + 0.315 us per MB of fp32 partials
-//       (8 S M N bytes: written, then read back).
+// model calibrated on the box with the weights streaming from HBM (every Qwen2.5-1.5B and -7B
+// projection at M = 8 .. 64 and every split of the down projections, each shape's weights
+// replicated past the 256 MB Infinity Cache; 276 timed points, mean error 5 %):
+//   t = 3.57 us + 1.41 us per round of workgroups (ceil(workgroups x S / CUs))
+//       + 0.0424 us (DKS 128) or 0.0357 us (DKS 256) per 1000 weight elements the busiest CU
+//       holds, counting a k-part's idle super-steps (rounds x 16 RT x KP x ceil(K / DKS / S /
+//       KP) x DKS), + 0.0087 us per 1000 of them when the kernel's registers or LDS leave one
+//       workgroup per CU (skinny_slots), + 0.0056 us per 1000 for each 16-token group past the
+//       first, + 0.052 us per MB of activations the workgroups read (each reads X over its part
+//       of K)
+//       + with S > 1: 3.89 us for the reduction launch + 0.223 us per MB of fp32 partials
+//       (8 S M N bytes: written, then read back); a split holds at least 8 super-steps (shorter
+//       ones measured slower than the model says: 1.5B down at M = 64, 14 splits 18.5 us, 8
+//       splits 16.1 us).
 // DKS = 256 only for one token group: with more its longer-lived registers cost a workgroup
 // per CU (gate|up of Qwen2.5-7B at M = 24: 42 us against 36 us at DKS = 128).  The activation
 // stages (2 x KP x 16 MT tokens x DKS x 2 bytes) must fit in LDS and a k-part of a split hold
@@ -2816,6 +2821,13 @@ bool rows_ok(int64_t m, const nf4_weight *ws, int nw) {
 // Plan::waves KP, Plan::bm 16 MT, Plan::dks DKS, Plan::splits S (tail_start 0: every tile
 // split); the cost (us) is returned through `cost`.
 constexpr bool skinny_fits(int kp, int mt, int dks) { return kp * mt * dks <= 2048; }
+
+// Workgroups per CU that a skinny kernel's registers and LDS allow (the compiler's register
+// counts for gfx950: 145 or more VGPRs leave 3 or fewer waves per SIMD, one 8-wave workgroup;
+// tests/test_skinny_occupancy.py checks this table against the compiled kernels).
+constexpr int skinny_slots(int mt, int rt, int dks) {
+    return (dks == 256 && rt <= 2) || (mt == 2 && rt == 1) || (mt == 4 && rt <= 4) ? 1 : 2;
+}
 
 // fx_only: only plans that can compute a LoRA down-projection of rank <= 16 in the launch (one
 // split, the stages 16 rows taller).
@@ -2831,7 +2843,7 @@ Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr
     for (const int dks : {256, 128}) {
         if (K % dks != 0 || (dks == 256 && mt > 1)) continue;
         const int64_t ss = K / dks;
-        const double per_elem = dks == 256 ? 0.0376 : 0.0416;
+        const double per_elem = dks == 256 ? 0.0357 : 0.0424;
         for (const auto &sh : kShapes) {
             const int rt = sh[0], kp = sh[1];
             if (!skinny_fits(kp, mt + (fx_only ? 1 : 0), dks)) continue;
@@ -2839,15 +2851,17 @@ Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr
             for (int i = 0; i < nw; ++i) wgs += (ws[i].rows + 16 * rt - 1) / (16 * rt);
             for (const int sp_try : {1, 2, 4, 8, 16}) {
                 const int64_t sps = (ss + sp_try - 1) / sp_try;  // super-steps per split
-                if (kp > 1 && sps < 2 * kp) break;
+                if ((kp > 1 && sps < 2 * kp) || (sp_try > 1 && sps < 8)) break;
                 const int sp = static_cast<int>((ss + sps - 1) / sps);  // no empty last split
                 if (fx_only && (sp > 1 || mt > 2)) break;
                 const int64_t per = (sps + kp - 1) / kp;
-                const double busy =
-                    double((wgs * sp + kCUs - 1) / kCUs) * 16.0 * rt * kp * per * dks / 1000.0;
+                const double rounds = double((wgs * sp + kCUs - 1) / kCUs);
+                const double busy = rounds * 16.0 * rt * kp * per * dks / 1000.0;
                 const double x_mb = double(wgs) * double(m) * double(K) * 2.0 / 1e6;
-                double t = 3.99 + busy * (per_elem + 0.0053 * (mt - 1)) + 0.0725 * x_mb;
-                if (sp > 1) t += 3.56 + 0.315 * 8.0 * sp * double(m) * double(n_out) / 1e6;
+                const double one_wg = skinny_slots(mt, rt, dks) == 1 ? 0.0087 : 0.0;
+                double t = 3.57 + 1.41 * rounds + busy * (per_elem + one_wg + 0.0056 * (mt - 1)) +
+                           0.052 * x_mb;
+                if (sp > 1) t += 3.89 + 0.223 * 8.0 * sp * double(m) * double(n_out) / 1e6;
                 if (t < best_t) {
                     best = Plan{7, 16 * rt, 16 * mt, sp, wgs, kp, sp > 1 ? 0 : wgs};
                     best.dks = dks;
@@ -2860,13 +2874,15 @@ Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr
     return best;
 }
 
-// The decode kernel's time by the same calibration (one workgroup per 16 rows, K split over
-// its waves): 4.26 us + 0.0637 us per 1000 elements of the busiest CU (+ 0.018 above 8 tokens).
+// The decode kernel's time (one workgroup per 16 rows, K split over its waves): 5.26 us +
+// 0.0637 us per 1000 elements of the busiest CU (+ 0.018 above 8 tokens); calibrated like the
+// skinny model, its fixed part raised by the 1 us that streaming the weights from HBM added to
+// its launches.
 double decode_cost(int64_t m, const nf4_weight *ws, int nw) {
     int64_t t16 = 0;
     for (int i = 0; i < nw; ++i) t16 += (ws[i].rows + 15) / 16;
     const double busiest = double((t16 + kCUs - 1) / kCUs) * 16.0 * double(ws[0].cols) / 1000.0;
-    return 4.26 + busiest * (m <= 8 ? 0.0637 : 0.0818);
+    return 5.26 + busiest * (m <= 8 ? 0.0637 : 0.0818);
 }
 
 // A skinny plan that can compute LoRA down-projections of rank <= 16 in its own launch: one

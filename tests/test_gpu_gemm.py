@@ -85,11 +85,11 @@ def test_decode_dequant_is_bit_exact(cuda, shape, bs, nested, dtype):
 SKINNY_CASES = [
     ((1200,), 2048, 16, 64, True),        # MT 1, RT 1 (8 k-parts), DKS 128
     ((5000,), 1024, 13, 64, True),        # MT 1, RT 2, DKS 128
-    ((5000,), 2048, 16, 128, False),      # MT 1, RT 2, DKS 256, block 128, fp32 absmax
+    ((5000,), 2048, 16, 128, False),      # MT 1, RT 2, DKS 128, block 128, fp32 absmax
     ((9000,), 768, 16, 64, True),         # MT 1, RT 4, DKS 128
     ((9000,), 1024, 16, 64, True),        # MT 1, RT 4, DKS 256
     ((8960, 8960), 1536, 16, 64, True),   # MT 1, RT 8, DKS 256: gate|up of Qwen2.5-1.5B
-    ((8960, 8960), 1536, 3, 64, True),    # MT 1, RT 2, DKS 128: the same at 3 tokens
+    ((8960, 8960), 1536, 3, 64, True),    # the same at 3 tokens
     ((1200,), 2048, 24, 64, True),        # MT 2, RT 1
     ((1200,), 1024, 17, 64, True),        # MT 2, RT 2
     ((700, 500), 512, 24, 64, True),      # MT 2, RT 4, two segments
@@ -98,7 +98,7 @@ SKINNY_CASES = [
     ((1200,), 512, 64, 64, True),         # MT 4, RT 4
     ((1200,), 256, 33, 64, True),         # MT 4, RT 8
     ((1024,), 8192, 16, 64, True),        # MT 1, RT 2, 8 reduction splits (fp32 partials)
-    ((1024,), 8960, 24, 64, True),        # MT 2, RT 4, 14 splits
+    ((1024,), 8960, 24, 64, True),        # MT 2, RT 2, 8 splits, the last one shorter
     ((1024,), 4096, 40, 64, True),        # MT 4, RT 2, 4 splits
     ((3584,), 18944, 8, 64, True),        # MT 1, RT 8, DKS 256, 8 splits, the last one shorter:
                                           # down of Qwen2.5-7B
