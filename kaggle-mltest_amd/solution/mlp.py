@@ -13,7 +13,10 @@ mirrored: this MLP always recomputes.
 
 `INT8_BACKWARD` (off by default, as RecomputedMLP's backward is fp16 in the reference) routes the
 input gradient through the int8 GEMMs of `int8_mlp` instead, the way the reference's fused
-decoder layer runs its MLP backward on the T4 (layer.py:530-534, 992-1013).
+decoder layer runs its MLP backward on the T4 (layer.py:530-534, 992-1013).  `INT8_FORWARD` (off
+by default, as in the reference, layer.py:531-533) computes gate|up in the forward through one
+int8 GEMM and the SwiGLU step (layer.py:900-912); the backward still recomputes gate|up in the
+GEMM dtype, as the reference's recomputing layers do (layer.py:986-990).
 """
 
 from __future__ import annotations
@@ -25,6 +28,8 @@ from .quant_state import nf4_state_ok
 
 # int8 input gradients (int8_mlp.mlp_input_grad_int8) in RecomputedMLP.backward
 INT8_BACKWARD = False
+# int8 gate|up product (int8_mlp.gate_up_fwd_int8) in RecomputedMLP.forward
+INT8_FORWARD = False
 
 
 # Token count from which the gate|up GEMM carries the SwiGLU epilogue (its tiles are the large
@@ -41,7 +46,12 @@ class RecomputedMLP(torch.autograd.Function):
             x2 = x2.contiguous()
         gate_w, up_w, down_w = gate_w.reshape(-1), up_w.reshape(-1), down_w.reshape(-1)
         inter = int(gate_qs.shape[0])
-        if x2.shape[0] >= FUSED_MIN_TOKENS:
+        if INT8_FORWARD and _int8_ok(gate_qs, down_qs):
+            from .int8_mlp import gate_up_fwd_int8
+
+            gu, hidden = gate_up_fwd_int8(x2, (gate_w, gate_qs), (up_w, up_qs))
+            del gu
+        elif x2.shape[0] >= FUSED_MIN_TOKENS:
             hidden = kernels.linear_swiglu_fwd(x2, (gate_w, gate_qs), (up_w, up_qs))
         else:
             gu = kernels.linear_fwd(x2, [(gate_w, gate_qs), (up_w, up_qs)])

@@ -570,6 +570,24 @@ def mlp_dx_int8(dh2, gu, gate_up, down, dtype: str = "f16"):
     return int8_scale(int8_matmul(q8, int8_weight_t(gate_up, cs_gu)), sq, cs_gu)
 
 
+def gate_up_fwd_int8(x, gate_up, dtype: str = "f16"):
+    """The int8 gate|up forward (layer.py:900-912 with gate_up_act_fwd_i8_kernel, 383-405;
+    without the 512-token chunking, which only bounds the T4's int32 buffer): x -> int8 rows
+    (sx), the stacked weights -> int8 rows (sw, nf4_int8_rows_kernel), the exact int32 product,
+    gu = round_dtype(fp32(acc) * sx[m] * sw[n]), and act = g / (1 + exp(-g)) * u in fp32 from
+    the rounded halves, rounded once.  Returns (gu [M, 2I], act [M, I]) as fp32 arrays holding
+    dtype values."""
+    x8, sx = int8_rows(x)
+    w8, sw = int8_weight_rows(gate_up)
+    gu = _round_to(int8_scale(int8_matmul(x8, w8), sx, sw), dtype)
+    inter = gu.shape[1] // 2
+    g, u = gu[:, :inter], gu[:, inter:]
+    f32 = np.float32
+    with np.errstate(over="ignore"):
+        act = (g / (f32(1.0) + np.exp(-g).astype(f32))).astype(f32)
+    return gu, _round_to((act * u).astype(f32), dtype)
+
+
 def rel_errors(out, ref) -> tuple[float, float]:
     """(max |out-ref| / max |ref|, mean |out-ref| / mean |ref|): the reference's ``_rel``
     (layer.py:1253-1254) and its mean counterpart."""

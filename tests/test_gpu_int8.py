@@ -184,3 +184,67 @@ def test_recomputed_mlp_int8_backward_switch(cuda, monkeypatch):
     err = ((x.grad.float().cpu() - xr.grad).abs().max() / xr.grad.abs().max()).item()
     print(f"RecomputedMLP int8 input gradient vs fp32: max |d| / max |ref| = {err:.4f}")
     assert err <= 6e-2, err
+
+
+@pytest.mark.parametrize("dtype,n,hidden,inter", [(torch.float16, 300, 1536, 8960),
+                                                  (torch.bfloat16, 5, 384, 640),
+                                                  (torch.float16, 1, 256, 128)])
+def test_gate_up_fwd_int8(cuda, dtype, n, hidden, inter):
+    """The int8 gate|up forward (layer.py:900-912): gate|up bit-exact against the oracle (int8
+    codes, exact int32 sums, scaling in the same order, one rounding), act within one rounding
+    of the oracle's in at most 1 % of the places (SiLU's exp may differ in its last bit)."""
+    from solution.int8_mlp import gate_up_fwd_int8
+
+    banner("int8 gate|up fwd", dtype, n, hidden, inter)
+    gate = random_weight(inter, hidden, seed=61, dev=cuda)
+    up = random_weight(inter, hidden, seed=62, dev=cuda)
+    g = torch.Generator().manual_seed(63)
+    x = (torch.randn(n, hidden, generator=g) * torch.logspace(-2, 1, n)[:, None]).to(dtype)
+    gu, act = gate_up_fwd_int8(x.to(cuda), gate, up)
+    assert gu.dtype == dtype and act.dtype == dtype
+    dt = "bf16" if dtype == torch.bfloat16 else "f16"
+    ref_gu, ref_act = o.gate_up_fwd_int8(x.float().numpy(), _ost([gate, up]), dt)
+    assert np.array_equal(gu.float().cpu().numpy(), ref_gu)
+    a = act.float().cpu().numpy()
+    ulp, tiny = (2.0 ** -7, 1e-38) if dt == "bf16" else (2.0 ** -10, 2.0 ** -24)
+    assert np.all(np.abs(a - ref_act) <= np.abs(ref_act) * ulp + tiny)
+    assert np.mean(a != ref_act) <= 1e-2
+
+
+def test_recomputed_mlp_int8_forward_switch(cuda, monkeypatch):
+    """RecomputedMLP with mlp.INT8_FORWARD: the output through the int8 gate|up product is the
+    oracle's int8 composite followed by the fp16 down GEMM, within 3e-2 of fp32 (per-token and
+    per-row 8-bit operands; the reference's self-check allows the int8 layer 2.5e-2 of its output,
+    residual included, layer.py:1410-1411); the backward recomputes gate|up in fp16, so the input
+    gradient is the one the fp16 forward gives, bit for bit."""
+    from solution import mlp
+    from solution.mlp import RecomputedMLP
+
+    banner("RecomputedMLP int8 forward")
+    hidden, inter, n = 1536, 8960, 300
+    gate = random_weight(inter, hidden, seed=71, dev=cuda)
+    up = random_weight(inter, hidden, seed=72, dev=cuda)
+    down = random_weight(hidden, inter, seed=73, dev=cuda)
+    wg, wu, wd = (torch.from_numpy(o.dequantize(*to_oracle_state(*t), "f16")).float()
+                  for t in (gate, up, down))
+    g = torch.Generator().manual_seed(74)
+    x0 = torch.randn(n, hidden, generator=g).half().to(cuda)
+    dy = (torch.randn(n, hidden, generator=g) * 1e-2).half().to(cuda)
+    outs, grads = [], []
+    for flag in (False, True):
+        monkeypatch.setattr(mlp, "INT8_FORWARD", flag)
+        x = x0.clone().requires_grad_()
+        out = RecomputedMLP.apply(x, gate[0], gate[1], up[0], up[1], down[0], down[1])
+        out.backward(dy)
+        outs.append(out.detach())
+        grads.append(x.grad)
+    assert torch.equal(grads[0], grads[1])
+    _, act = o.gate_up_fwd_int8(x0.float().cpu().numpy(), _ost([gate, up]), "f16")
+    via = torch.from_numpy(act) @ wd.t()
+    mx, _ = o.rel_errors(outs[1], via)
+    assert mx <= 1e-2, mx
+    ref = o.mlp_fwd(x0.float().cpu(), wg, wu, wd)
+    mx, mean = o.rel_errors(outs[1], ref)
+    print(f"RecomputedMLP int8 forward vs fp32: max rel {mx:.4f}, mean rel {mean:.4f}")
+    assert mx <= 3e-2, mx
+    assert not torch.equal(outs[0], outs[1])

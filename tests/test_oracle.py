@@ -441,3 +441,27 @@ def test_int8_mlp_dx_against_fp32():
     ref = torch.cat([dact * uu * sig * (1 + gg * (1 - sig)), dact * gg * sig], 1) @ torch.cat([wg, wu])
     err = np.abs(dy2 - ref.numpy()).max() / np.abs(ref.numpy()).max()
     assert err <= 3e-2, err
+
+
+def test_int8_gate_up_fwd_against_fp32():
+    """The int8 gate|up forward: gate|up within 2e-2 of the largest fp32 product (the
+    reference's own bound for one int8 product, test_kernels.py:350) and on the dtype's grid;
+    act against torch's fp32 SiLU (torch.nn.functional.silu, a library routine) times up on the
+    rounded halves, within one rounding to the dtype.  A swapped gate / up, a scale taken per
+    column instead of per row, or a missing rounding of the halves fails one of these."""
+    ws = _i8_weights(14, [(256, 192), (256, 192)])
+    g = np.random.default_rng(15)
+    x = torch.from_numpy((g.standard_normal((40, 192)) * np.logspace(-2, 1, 40)[:, None])
+                         .astype(np.float32)).half()
+    w = torch.from_numpy(o.stack_f32(ws))
+    ref = x.float() @ w.t()
+    for dt, ulp, tiny in (("f16", 2.0 ** -10, 2.0 ** -24), ("bf16", 2.0 ** -7, 1e-38)):
+        gu, act = o.gate_up_fwd_int8(x.float().numpy(), ws, dt)
+        assert gu.shape == (40, 512) and act.shape == (40, 256)
+        err = np.abs(gu - ref.numpy()).max(axis=1) / np.abs(ref.numpy()).max(axis=1)
+        assert err.max() <= 2e-2, err.max()
+        assert np.array_equal(o._round_to(gu, dt), gu)
+        gg, uu = torch.from_numpy(gu[:, :256]), torch.from_numpy(gu[:, 256:])
+        want = (torch.nn.functional.silu(gg) * uu).numpy()
+        assert np.all(np.abs(act - want) <= np.abs(want) * ulp + tiny)  # tiny: fp16 subnormals
+        assert np.array_equal(o._round_to(act, dt), act)
