@@ -2520,12 +2520,25 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *partial,
         const int64_t base = m * n_out + c0;
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         if (vec && nc == 4) {
-            for (int s = 0; s < splits; ++s) {
-                const float4_t t = *reinterpret_cast<const float4_t *>(partial + s * total + base);
-                v[0] += t.x;
-                v[1] += t.y;
-                v[2] += t.z;
-                v[3] += t.w;
+            // the loads of 8 splits go out together (the partials come from other XCDs' writes,
+            // one memory latency each: issued one by one they cost a latency per split), then
+            // are added in split order
+            constexpr int U = 8;
+            for (int s0 = 0; s0 < splits; s0 += U) {
+                float4_t t[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    t[u] = s0 + u < splits
+                               ? *reinterpret_cast<const float4_t *>(partial + (s0 + u) * total + base)
+                               : (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    if (s0 + u >= splits) break;
+                    v[0] += t[u].x;
+                    v[1] += t[u].y;
+                    v[2] += t[u].z;
+                    v[3] += t[u].w;
+                }
             }
         } else {
             for (int s = 0; s < splits; ++s)
@@ -2809,8 +2822,11 @@ bool rows_ok(int64_t m, const nf4_weight *ws, int nw) {
 //       workgroup per CU (skinny_slots), + 0.0056 us per 1000 for each 16-token group past the
 //       first, + 0.052 us per MB of activations the workgroups read (each reads X over its part
 //       of K)
-//       + with S > 1: 3.89 us for the reduction launch + 0.223 us per MB of fp32 partials
-//       (8 S M N bytes: written, then read back); a split holds at least 8 super-steps (shorter
+//       + with S > 1: 2.4 us for the reduction launch (3.89 us before its loads of 8 splits
+//       went out together; re-timed: 1.5B down at M = 8 11.4 us with 8 splits against 12.7 us
+//       unsplit, 7B gate|up at M = 64 56.3 us with 2 splits against 57.5 us, 7B o at M = 64
+//       15.4 against 16.3) + 0.223 us per MB of fp32 partials (8 S M N bytes: written, then
+//       read back); a split holds at least 8 super-steps (shorter
 //       ones measured slower than the model says: 1.5B down at M = 64, 14 splits 18.5 us, 8
 //       splits 16.1 us).
 // DKS = 256 only for one token group: with more its longer-lived registers cost a workgroup
@@ -2861,7 +2877,7 @@ Plan plan_skinny(int64_t m, const nf4_weight *ws, int nw, double *cost = nullptr
                 const double one_wg = skinny_slots(mt, rt, dks) == 1 ? 0.0087 : 0.0;
                 double t = 3.57 + 1.41 * rounds + busy * (per_elem + one_wg + 0.0056 * (mt - 1)) +
                            0.052 * x_mb;
-                if (sp > 1) t += 3.89 + 0.223 * 8.0 * sp * double(m) * double(n_out) / 1e6;
+                if (sp > 1) t += 2.4 + 0.223 * 8.0 * sp * double(m) * double(n_out) / 1e6;
                 if (t < best_t) {
                     best = Plan{7, 16 * rt, 16 * mt, sp, wgs, kp, sp > 1 ? 0 : wgs};
                     best.dks = dks;
