@@ -2911,10 +2911,11 @@ bool skinny_fx_ok(const Plan &p, int xa_rank) {
            skinny_fits(p.waves, mt + 1, p.dks);
 }
 
-// A standalone LoRA down-projection launch (nf4_lora_xa_multi, two adapters at decode token
-// counts), timed on the box: ~2.8 us + 1.1 ns per reduction element, and ~1.5 us between
-// launches.
-double xa_launch_cost(int64_t k) { return 4.3 + 0.00108 * double(k); }
+// A standalone LoRA down-projection launch (nf4_lora_xa_multi at up to 64 tokens: one
+// workgroup per adapter, A row and 8 tokens), timed on the box back to back in a graph (the gap
+// between launches included): 3.1 us at K = 1536, 4.2 us at K = 3584, at every token count to
+// 64; + 0.5 us of margin.
+double xa_launch_cost(int64_t k) { return 2.8 + 0.00054 * double(k); }
 constexpr double kFxCost = 2.0;
 
 // The skinny plan for the call: when it has LoRA down-projections to compute (xa_rank > 0: rank

@@ -173,21 +173,26 @@ __global__ __launch_bounds__(kRowdotWaves * 64) void rowdot_kernel(const Jobs jo
 }
 
 // Decode-size xa (M <= kRowvecMaxM tokens): out[m][j] = scale * sum_k act[m][k] A[j][k] with one
-// workgroup per (job, row j of A) over the whole reduction, instead of one workgroup per job:
-// each of 256 threads takes 8 consecutive k per 2048-wide step (16-byte loads of the A row and
-// of every token's activations), accumulates with v_dot2 in fp32, and the workgroup adds its
-// lanes in a fixed order (DPP inside each wave, then the four waves in order).  Needs 16-byte
-// aligned rows (Job::vec == 3).
-constexpr int64_t kRowvecMaxM = 8;
+// workgroup per (job, row j of A, group of MT tokens) over the whole reduction, instead of one
+// workgroup per 16 tokens and job: each of 256 threads takes 8 consecutive k per 2048-wide step
+// (16-byte loads of the A row and of every token's activations), accumulates with v_dot2 in
+// fp32, and the workgroup adds its lanes in a fixed order (DPP inside each wave, then the four
+// waves in order).  The MFMA kernel above streams A and 16 tokens through a single CU per 16
+// tokens (K = 3584: 8.2 us for 16 tokens, whatever M up to 64); here the rank x token-group
+// workgroups spread them over the GPU.  Needs 16-byte aligned rows (Job::vec == 3).
+constexpr int64_t kRowvecMaxM = 64;
 
 template <int DT, int MT>
-__global__ __launch_bounds__(256) void rowvec_kernel(const Jobs jobs, int64_t m) {
+__global__ __launch_bounds__(256) void rowvec_kernel(const Jobs jobs, int64_t m_all) {
     __shared__ float red[4][MT];
     const Job &jb = jobs.j[blockIdx.y];
     const int64_t k = jb.cols, ld = jb.ld;
     const int rank = static_cast<int>(gridDim.x);
     const int j = blockIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.z) * MT;  // this workgroup's first token
+    const int64_t m = m_all - t0 < MT ? m_all - t0 : MT;
     const uint16_t *w = jb.w + j * k;
+    const uint16_t *in = jb.in + t0 * ld;
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
@@ -197,7 +202,7 @@ __global__ __launch_bounds__(256) void rowvec_kernel(const Jobs jobs, int64_t m)
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             if (t >= m) break;
-            const u32x4_t x = *reinterpret_cast<const u32x4_t *>(jb.in + t * ld + k0);
+            const u32x4_t x = *reinterpret_cast<const u32x4_t *>(in + t * ld + k0);
             acc[t] = dot2<DT>(a.w, x.w, dot2<DT>(a.z, x.z, dot2<DT>(a.y, x.y, dot2<DT>(a.x, x.x, acc[t]))));
         }
     }
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(256) void rowvec_kernel(const Jobs jobs, int64_t m)
     if (threadIdx.x < MT && threadIdx.x < m) {
         const int t = threadIdx.x;
         const float v = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
-        static_cast<uint16_t *>(jb.out)[t * rank + j] = st1<DT>(v * jb.scale);
+        static_cast<uint16_t *>(jb.out)[(t0 + t) * rank + j] = st1<DT>(v * jb.scale);
     }
 }
 
@@ -631,8 +636,9 @@ int rowdot_multi(const nf4_lora_job *jobs, int njobs, int64_t m, int rank, int d
     bool vec = true;
     for (int i = 0; i < njobs; ++i) vec = vec && J.j[i].vec == 3;
     if (!B_LAYOUT && vec && m <= kRowvecMaxM) {
-        const dim3 grid(static_cast<unsigned>(rank), static_cast<unsigned>(njobs));
         const int mt = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+        const dim3 grid(static_cast<unsigned>(rank), static_cast<unsigned>(njobs),
+                        static_cast<unsigned>((m + mt - 1) / mt));
 #define NF4_ROWVEC(DT, MT) hipLaunchKernelGGL((rowvec_kernel<DT, MT>), grid, dim3(256), 0, s, J, m)
         if (dtype == NF4_BF16) {
             if (mt == 1) NF4_ROWVEC(NF4_BF16, 1);

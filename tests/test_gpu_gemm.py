@@ -346,11 +346,12 @@ def test_forward_computes_lora_down_projection(cuda, shape, m, r, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m,k,r", [(1, 3584, 16), (2, 1536, 16), (5, 2056, 8), (8, 4096, 16),
-                                   (9, 1536, 16)])
+                                   (9, 1536, 16), (13, 3584, 12), (40, 2056, 16), (64, 3584, 16),
+                                   (65, 1536, 16)])
 def test_lora_xa_decode_sizes(cuda, dtype, m, k, r):
-    """t = x A^T at decode token counts (up to 8 tokens: one workgroup per (adapter, A row);
-    9 tokens: the MFMA kernel), two adapters in one launch, against an fp32 product; K not a
-    multiple of the 2048-wide step."""
+    """t = x A^T at decode token counts (up to 64 tokens: one workgroup per (adapter, A row,
+    group of up to 8 tokens), the last group partly used; 65 tokens: the MFMA kernel), two
+    adapters in one launch, against an fp32 product; K not a multiple of the 2048-wide step."""
     from solution import kernels
 
     banner("lora xa decode", dtype, m, k, r)
