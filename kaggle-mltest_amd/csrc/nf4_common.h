@@ -144,6 +144,73 @@ __device__ __forceinline__ Nf4Table make_table(const float (&code)[16], float s)
     return r;
 }
 
+// Half tables.  Where the two lanes of a pair (lane, lane ^ 1) dequantize the same absmax block,
+// lane h of the pair forms the entries 8h .. 8h + 7 of the block's table and receives the other
+// eight from its partner by a DPP swap: 8 products, 4 conversions, 4 perms and 4 swaps per lane
+// instead of 16, 8 and 8.  Slots 0-1 hold the lane's own half and slots 2-3 its partner's, so
+// on the odd lane the entry of nibble n sits where the full table keeps n ^ 8: its lookups flip
+// bit 3 through the selector base (lookup4s).
+struct Nf4HalfCodes {
+    float c[8];        // code[8h + i]
+    uint32_t selbase;  // byte i: i (even lane) or 4 + i (odd lane)
+};
+
+__device__ __forceinline__ Nf4HalfCodes half_codes(const float (&code)[16]) {
+    const bool odd = (threadIdx.x & 1) != 0;
+    Nf4HalfCodes h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h.c[i] = odd ? code[8 + i] : code[i];
+    h.selbase = odd ? 0x07060504u : 0x03020100u;
+    return h;
+}
+
+// v from lane ^ 1 (quad_perm [1, 0, 3, 2])
+__device__ __forceinline__ uint32_t swap_pair(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, true));
+}
+
+template <int DT>
+__device__ __forceinline__ Nf4Table make_table_half(const Nf4HalfCodes &hc, float s) {
+    uint32_t t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = pack2<DT>(__fmul_rn(hc.c[2 * j], s), __fmul_rn(hc.c[2 * j + 1], s));
+    Nf4Table r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        r.lo[k] = vperm(t[2 * k + 1], t[2 * k], kPermLoBytes);
+        r.hi[k] = vperm(t[2 * k + 1], t[2 * k], kPermHiBytes);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        r.lo[2 + k] = swap_pair(r.lo[k]);
+        r.hi[2 + k] = swap_pair(r.hi[k]);
+    }
+    return r;
+}
+
+// 4 nibbles s (one per byte, element order) -> 4 table entries as two packed pairs; `selbase`
+// picks the half of the table that bit 3 of a nibble selects (0x03020100 for a full table).
+__device__ __forceinline__ void lookup4s(const Nf4Table &t, uint32_t s, uint32_t selbase,
+                                         uint32_t &o0, uint32_t &o1) {
+    const uint32_t s7 = s & 0x07070707u;
+    const uint32_t sel = ((s >> 1) & 0x04040404u) ^ selbase;  // one v_bitop3
+    const uint32_t lo = vperm(vperm(t.lo[3], t.lo[2], s7), vperm(t.lo[1], t.lo[0], s7), sel);
+    const uint32_t hi = vperm(vperm(t.hi[3], t.hi[2], s7), vperm(t.hi[1], t.hi[0], s7), sel);
+    o0 = vperm(hi, lo, 0x05010400u);
+    o1 = vperm(hi, lo, 0x07030602u);
+}
+
+// The 8 elements of one packed dword through a half table (lookup8 below, selector base of
+// the lane's half).
+__device__ __forceinline__ u32x4_t lookup8s(const Nf4Table &t, uint32_t p, uint32_t selbase) {
+    const uint32_t hi4 = (p >> 4) & 0x0F0F0F0Fu;
+    const uint32_t lo4 = p & 0x0F0F0F0Fu;
+    uint32_t o0, o1, o2, o3;
+    lookup4s(t, vperm(lo4, hi4, 0x05010400u), selbase, o0, o1);
+    lookup4s(t, vperm(lo4, hi4, 0x07030602u), selbase, o2, o3);
+    return (u32x4_t){o0, o1, o2, o3};
+}
+
 // 4 nibbles s (one per byte, element order) -> 4 table entries as two packed pairs.
 __device__ __forceinline__ void lookup4(const Nf4Table &t, uint32_t s, uint32_t &o0, uint32_t &o1) {
     const uint32_t s7 = s & 0x07070707u;

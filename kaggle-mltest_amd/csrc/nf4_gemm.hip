@@ -701,12 +701,14 @@ struct FwdWeight {
     }
 
     // Dword `part` of the 16 packed bytes (8 elements) through the register table of this
-    // thread's row (make_table with the row's absmax).
-    __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, int part) const {
+    // thread's row: the half table (make_table_half) that this thread and its partner, the other
+    // half of the row's 64-deep step (thread t ^ 1), build together.
+    __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, uint32_t selbase,
+                                               int part) const {
         const int t = threadIdx.x % (2 * BP);
         const int row = t >> 1, h = (t & 1) * 4;
         const uint32_t wd = part == 0 ? raw.x : part == 1 ? raw.y : part == 2 ? raw.z : raw.w;
-        *reinterpret_cast<u32x4_t *>(s + swz(row, h + part)) = lookup8(tb, wd);
+        *reinterpret_cast<u32x4_t *>(s + swz(row, h + part)) = lookup8s(tb, wd, selbase);
     }
 };
 
@@ -752,11 +754,13 @@ struct DxWeight {
         abs = absmax_bload(r, ad.block + static_cast<int>(n0 * (K >> r.bs_shift)));
     }
 
-    __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, int part) const {
+    // through the half table shared with thread t ^ 1 (the other 32 k of the same absmax block)
+    __device__ __forceinline__ void store_part(uint8_t *s, const Nf4Table &tb, uint32_t selbase,
+                                               int part) const {
         const int t = threadIdx.x % (2 * BP);
         const int n = t / KQ, c = (t % KQ) * 4 + part;
         const uint32_t wd = part == 0 ? raw.x : part == 1 ? raw.y : part == 2 ? raw.z : raw.w;
-        *reinterpret_cast<u32x4_t *>(s + swz_t<BP>(n, c)) = lookup8(tb, wd);
+        *reinterpret_cast<u32x4_t *>(s + swz_t<BP>(n, c)) = lookup8s(tb, wd, selbase);
     }
 };
 
@@ -1001,6 +1005,7 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
     const float *code2 = s_code2[PAIR ? wseg : 0];
     float code_r[16];
     load_code_sgpr(w.code, code_r);
+    const Nf4HalfCodes hc = half_codes(code_r);
 
     const int wp = wave % WP, wm = wave / WP;
     const int lane = threadIdx.x & 63;
@@ -1112,9 +1117,9 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
     uint8_t *sA[2] = {sT[g][0] + BP * ROWB, sT[g][1] + BP * ROWB};
     if (nv > 0) {
         {
-            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
+            const Nf4Table tb = make_table_half<DT>(hc, absmax_val(w, wt[0].abs, code2));
 #pragma unroll
-            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
+            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, hc.selbase, q);
         }
         wait_dma();
         __syncthreads();
@@ -1122,10 +1127,10 @@ __device__ __forceinline__ void fwd_body(const GemmArgs &a, const TileMap &tm, u
         for (; v + 1 < nv; v += 2) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
+                const Nf4Table tb = make_table_half<DT>(hc, absmax_val(w, wt[b ^ 1].abs, code2));
                 mma_step_interleaved<DT, TP, TM, PH>(
                     acc, sW[b], sA[b], prow0, wm * (BM / WM), [&](int ks) {
-                        wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                        wt[b ^ 1].store_part(sW[b ^ 1], tb, hc.selbase, ks);
                         if (ks == 0) {
                             dma_a(b ^ 1, v + b + 1);
                             stage(b, v + b + 2);
@@ -2377,6 +2382,7 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
         const float *code2 = s_code2[seg];
         float code_r[16];
         load_code_sgpr(w.code, code_r);
+        const Nf4HalfCodes hc = half_codes(code_r);
         auto dma_a = [&](int b, int64_t v) {  // dY columns of step v into LDS stage b
             const int64_t st = b0 + g + KG * v;
             const rsrc_t rs = KG > 1 && st >= e0 ? ar0 : ar;
@@ -2426,9 +2432,9 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
         stage(0, 0);
         stage(1, 1);
         {
-            const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[0].abs, code2));
+            const Nf4Table tb = make_table_half<DT>(hc, absmax_val(w, wt[0].abs, code2));
 #pragma unroll
-            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, q);
+            for (int q = 0; q < 4; ++q) wt[0].store_part(sW[0], tb, hc.selbase, q);
         }
         wait_dma();
         __syncthreads();
@@ -2437,10 +2443,10 @@ __device__ __forceinline__ void dx_body(const GemmArgs &a, const TileMap &tm, ui
         for (; v + 1 < nv; v += 2) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, wt[b ^ 1].abs, code2));
+                const Nf4Table tb = make_table_half<DT>(hc, absmax_val(w, wt[b ^ 1].abs, code2));
                 mma_step_dx<DT, BP, TP, TM>(
                     acc, sW[b], sA[b], wp * (BP / WP), wm * (BM / WM), [&](int ks) {
-                        wt[b ^ 1].store_part(sW[b ^ 1], tb, ks);
+                        wt[b ^ 1].store_part(sW[b ^ 1], tb, hc.selbase, ks);
                         if (ks == 0) {
                             dma_a(b ^ 1, v + b + 1);
                             stage(b, v + b + 2);
