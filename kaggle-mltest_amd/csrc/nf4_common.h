@@ -188,6 +188,44 @@ __device__ __forceinline__ Nf4Table make_table_half(const Nf4HalfCodes &hc, floa
     return r;
 }
 
+// The same for the pair (lane, lane ^ 16), the partner's half through the LDS crossbar
+// (ds_swizzle, xor mask 16 within each 32 lanes; no LDS memory): lane bit 4 picks the half.
+__device__ __forceinline__ Nf4HalfCodes half_codes16(const float (&code)[16]) {
+    const bool odd = (threadIdx.x & 16) != 0;
+    Nf4HalfCodes h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h.c[i] = odd ? code[8 + i] : code[i];
+    h.selbase = odd ? 0x07060504u : 0x03020100u;
+    return h;
+}
+
+__device__ __forceinline__ uint32_t swap_lane16(uint32_t v) {
+    // bit mode: and 0x1f, or 0, xor 0x10
+    return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F));
+}
+
+template <int DT>
+__device__ __forceinline__ Nf4Table make_table_half16(const Nf4HalfCodes &hc, float s) {
+    uint32_t t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = pack2<DT>(__fmul_rn(hc.c[2 * j], s), __fmul_rn(hc.c[2 * j + 1], s));
+    Nf4Table r;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        r.lo[k] = vperm(t[2 * k + 1], t[2 * k], kPermLoBytes);
+        r.hi[k] = vperm(t[2 * k + 1], t[2 * k], kPermHiBytes);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        r.lo[2 + k] = swap_lane16(r.lo[k]);
+        r.hi[2 + k] = swap_lane16(r.hi[k]);
+    }
+    return r;
+}
+
+// 8 elements of a packed dword in nibble-plane order (lookup8_planes) through a half table.
+__device__ __forceinline__ u32x4_t lookup8_planes_s(const Nf4Table &t, uint32_t p, uint32_t selbase);
+
 // 4 nibbles s (one per byte, element order) -> 4 table entries as two packed pairs; `selbase`
 // picks the half of the table that bit 3 of a nibble selects (0x03020100 for a full table).
 __device__ __forceinline__ void lookup4s(const Nf4Table &t, uint32_t s, uint32_t selbase,
@@ -240,6 +278,13 @@ __device__ __forceinline__ u32x4_t lookup8_planes(const Nf4Table &t, uint32_t p)
     uint32_t o0, o1, o2, o3;
     lookup4(t, (p >> 4) & 0x0F0F0F0Fu, o0, o1);
     lookup4(t, p & 0x0F0F0F0Fu, o2, o3);
+    return (u32x4_t){o0, o1, o2, o3};
+}
+
+__device__ __forceinline__ u32x4_t lookup8_planes_s(const Nf4Table &t, uint32_t p, uint32_t selbase) {
+    uint32_t o0, o1, o2, o3;
+    lookup4s(t, (p >> 4) & 0x0F0F0F0Fu, selbase, o0, o1);
+    lookup4s(t, p & 0x0F0F0F0Fu, selbase, o2, o3);
     return (u32x4_t){o0, o1, o2, o3};
 }
 

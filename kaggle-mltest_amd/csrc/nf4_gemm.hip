@@ -1584,6 +1584,14 @@ void decode_kernel(const GemmArgs a) {
 // doubles the weight bytes in flight; its stages need twice the LDS.
 constexpr int64_t kSkinnyMaxM = 64;
 
+// Half tables (make_table_half16) at DKS = 128, except where their 8 code registers per lane
+// would cost a workgroup per CU (the register counts of the compiled kernels: 1 token group x
+// 8 k-parts, 2 x 2 row tiles, 4 x 8 row tiles, and 2 x 8 with the down-projection in the launch).
+constexpr bool skinny_half(int mt, int rt, int kp, int dks, bool fx) {
+    return dks == 128 && !(mt == 1 && kp == 8 && !fx) && !(mt == 2 && rt == 2 && !fx) &&
+           !(mt == 4 && rt == 8) && !(mt == 2 && rt == 8 && fx);
+}
+
 template <int DT, int MT, int RT, int KP, int DKS, bool FX>
 __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) {
     constexpr int NW = RT * KP, NT = NW * 64, MP = 16 * MT;
@@ -1634,6 +1642,8 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
     for (int i = threadIdx.x; i < 256; i += NT) s_code2[i] = code2_entry(w, i);
     float code_r[16];
     load_code_sgpr(w.code, code_r);
+    // lane groups g and g ^ 1 cover one absmax block at DKS = 128 (skinny_half below)
+    const Nf4HalfCodes hc = half_codes16(code_r);
 
     // weights: DKS / 8 packed bytes of this lane's row per super-step; a wave's loads past its
     // part repeat its last super-step (cached bytes, never used)
@@ -1730,13 +1740,17 @@ __global__ __launch_bounds__(RT * KP * 64) void skinny_kernel(const GemmArgs a) 
     __syncthreads();  // code2 table, activation stage 0
 
     auto compute = [&](const WStage &s, int b) {
-        const Nf4Table tb = make_table<DT>(code_r, absmax_val(w, s.abs, s_code2));
+        // DKS = 128: the lane groups g and g ^ 1 cover the two halves of one absmax block and
+        // build its table together (make_table_half16)
+        constexpr bool HALF = skinny_half(MT, RT, KP, DKS, FX);
+        const Nf4Table tb = HALF ? make_table_half16<DT>(hc, absmax_val(w, s.abs, s_code2))
+                                 : make_table<DT>(code_r, absmax_val(w, s.abs, s_code2));
         const uint8_t *xb = s_x + b * XSTG + kp * RS * XROW;
 #pragma unroll
         for (int ks = 0; ks < NSUB; ++ks) {
             const u32x4_t &raw = s.raw[ks / 4];
             const uint32_t wd = ks % 4 == 0 ? raw.x : ks % 4 == 1 ? raw.y : ks % 4 == 2 ? raw.z : raw.w;
-            const u32x4_t fa = lookup8_planes(tb, wd);
+            const u32x4_t fa = HALF ? lookup8_planes_s(tb, wd, hc.selbase) : lookup8_planes(tb, wd);
             u32x4_t fa_t = (u32x4_t){0u, 0u, 0u, 0u};
             if (FX && fx_wave)
                 fa_t = *reinterpret_cast<const u32x4_t *>(xb + (MP + r) * XROW + (((NSUB * g + ks) ^ r) << 4));
