@@ -484,11 +484,16 @@ def qkv_rope_bwd(dq: torch.Tensor, dk: torch.Tensor, dv: torch.Tensor, cos: torc
 
 
 def make_lora(seg: int, rank: int, scale: float, t=None, b=None, a=None, da=None) -> NF4Lora:
-    return NF4Lora(seg=seg, rank=rank, scale=float(scale),
-                   t=t.data_ptr() if t is not None else None,
-                   b=b.data_ptr() if b is not None else None,
-                   a=a.data_ptr() if a is not None else None,
-                   da=da.data_ptr() if da is not None else None)
+    """The adapter struct of segment `seg`.  It holds raw pointers, so it also keeps references
+    to its tensors: a temporary passed here (t=lora_xa(...)) stays allocated while the struct
+    lives, instead of returning to torch's cache where the call's own output could reuse it."""
+    lo = NF4Lora(seg=seg, rank=rank, scale=float(scale),
+                 t=t.data_ptr() if t is not None else None,
+                 b=b.data_ptr() if b is not None else None,
+                 a=a.data_ptr() if a is not None else None,
+                 da=da.data_ptr() if da is not None else None)
+    lo._tensors = (t, b, a, da)
+    return lo
 
 
 __all__ = ["dequant", "linear_fwd", "linear_dx", "lora_xa", "lora_da", "lora_wgrad",

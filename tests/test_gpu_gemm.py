@@ -300,7 +300,8 @@ def test_small_m_stacked_bias_lora(cuda, m, dtype):
     bd = _x(1, 136, 35, cuda, dtype, std=0.5).view(-1)
     ad = ((torch.rand(r, 8960, generator=g) * 2 - 1) / 8960 ** 0.5).to(dtype).to(cuda)
     bbd = (torch.randn(40, r, generator=g) * 0.05).to(dtype).to(cuda)
-    yd = kernels.linear_fwd(xd, segs_d, bd, [kernels.make_lora(1, r, s, t=kernels.lora_xa(xd, ad), b=bbd)])
+    td = kernels.lora_xa(xd, ad)
+    yd = kernels.linear_fwd(xd, segs_d, bd, [kernels.make_lora(1, r, s, t=td, b=bbd)])
     assert_rel(yd, o.linear_fwd(xd, wd, bd, [(96, 40, xd, ad, bbd, s)]), what="small-M long K")
 
 

@@ -95,6 +95,26 @@ def test_kernels_refuse_cpu_tensors_loudly():
         NF4Linear.apply(x, packed.view(-1), qs, None)
 
 
+def test_lora_struct_keeps_its_tensors_alive():
+    """make_lora stores raw pointers; a temporary passed to it (t=lora_xa(...)) must not return
+    to torch's cache while the struct is in use, or the call's own output may be allocated over
+    it.  The struct holds references: the tensor outlives the caller's last name for it."""
+    import gc
+    import weakref
+
+    from solution import kernels
+
+    t = torch.empty(4, 16, dtype=torch.float16)
+    ref = weakref.ref(t)
+    lo = kernels.make_lora(0, 16, 2.0, t=t, b=torch.empty(8, 16, dtype=torch.float16))
+    del t
+    gc.collect()
+    assert ref() is not None and lo.t == ref().data_ptr()
+    del lo
+    gc.collect()
+    assert ref() is None
+
+
 def test_missing_library_raises(tmp_path):
     from solution import _lib
 
