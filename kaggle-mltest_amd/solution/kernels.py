@@ -117,8 +117,9 @@ def linear_fwd(x: torch.Tensor, weights, bias: torch.Tensor | None = None, loras
                out: torch.Tensor | None = None, tile: int | None = None,
                splits: int = 1) -> torch.Tensor:
     """Y[M, sum rows] = x[M, K] @ W_stack^T (+ bias) (+ LoRA terms).  `loras`: NF4Lora structs
-    whose pointers stay alive for the call (the caller keeps the tensors).  `tile` (TILE_*)
-    and `splits` pin the tiling; None lets the library choose."""
+    whose pointers stay alive for the call (make_lora's structs hold their tensors; a struct
+    built otherwise needs the caller to keep them).  `tile` (TILE_*) and `splits` pin the
+    tiling; None lets the library choose."""
     _check_device(x, bias)
     dt = _code(x.dtype)
     m, k = x.shape
