@@ -24,6 +24,26 @@ def cuda():
     return torch.device("cuda:0")
 
 
+@pytest.fixture(scope="session")
+def gemm_asm(tmp_path_factory):
+    """nf4_gemm.hip compiled for gfx950 to assembly, once per session (hipcc cross-compiles
+    without a GPU): the text, read by the tests of register counts and wait placement."""
+    import subprocess
+
+    import build
+
+    try:
+        hipcc = build.hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("asm") / "nf4_gemm.s"
+    cmd = [hipcc, *build.FLAGS, "--offload-device-only", "-S", str(PKG / "csrc" / "nf4_gemm.hip"),
+           "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    return out.read_text()
+
+
 def pytest_collection_modifyitems(config, items):
     # GPU tests print their case before running, so a GPU fault names it.
     os.environ.setdefault("PYTHONUNBUFFERED", "1")

@@ -14,20 +14,9 @@ target) through an in-order model of the vmcnt counter and checks that no instru
 writes a register that an inline-assembly load still in flight is to write."""
 
 import re
-import subprocess
 
 import pytest
 
-from tests.conftest import PKG
-
-
-def _hipcc():
-    import build
-
-    try:
-        return build.hipcc()
-    except RuntimeError:
-        return None
 
 
 def _kernels(asm: str):
@@ -100,21 +89,9 @@ def _check(lines, barriers_allowed=0):
 
 
 @pytest.fixture(scope="module")
-def kernels(tmp_path_factory):
-    """(name, lines) of every forward and input-gradient kernel of nf4_gemm.hip, compiled once
-    for the module."""
-    hipcc = _hipcc()
-    if hipcc is None:
-        pytest.skip("hipcc not available")
-    import build
-
-    out = tmp_path_factory.mktemp("asm") / "nf4_gemm.s"
-    cmd = [hipcc, *build.FLAGS, "--offload-device-only", "-S", str(PKG / "csrc" / "nf4_gemm.hip"),
-           "-o", str(out)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    assert res.returncode == 0, res.stderr[-2000:]
-    ks = [(k, b) for k, b in _kernels(out.read_text())
-          if re.search(r"(fwd|dx)_(head_tail_|rw_)?kernel", k)]
+def kernels(gemm_asm):
+    """(name, lines) of every forward and input-gradient kernel of nf4_gemm.hip."""
+    ks = [(k, b) for k, b in _kernels(gemm_asm) if re.search(r"(fwd|dx)_(head_tail_|rw_)?kernel", k)]
     assert len(ks) >= 8
     return ks
 

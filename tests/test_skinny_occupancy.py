@@ -8,11 +8,9 @@ at most 8 waves per SIMD, 2 waves per SIMD for each 8-wave workgroup; LDS from
 `.group_segment_fixed_size` against 160 KB), and checks it against the table."""
 
 import re
-import subprocess
 
 import pytest
 
-from tests.conftest import PKG
 
 
 def table_slots(mt, rt, dks):
@@ -37,20 +35,9 @@ def _metadata(asm: str):
 
 
 @pytest.mark.timeout(600)
-def test_skinny_slots_match_the_compiled_kernels(tmp_path):
-    import build
-
-    try:
-        hipcc = build.hipcc()
-    except RuntimeError:
-        pytest.skip("hipcc not available")
-    out = tmp_path / "nf4_gemm.s"
-    cmd = [hipcc, *build.FLAGS, "--offload-device-only", "-S", str(PKG / "csrc" / "nf4_gemm.hip"),
-           "-o", str(out)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    assert res.returncode == 0, res.stderr[-2000:]
+def test_skinny_slots_match_the_compiled_kernels(gemm_asm):
     checked = 0
-    for name, f in _metadata(out.read_text()).items():
+    for name, f in _metadata(gemm_asm).items():
         m = re.search(r"skinny_kernelILi(\d)ELi(\d)ELi(\d)ELi(\d)ELi(\d+)ELb([01])E", name)
         if not m or m.group(6) == "1":
             continue
