@@ -504,10 +504,13 @@ __all__ = ["dequant", "linear_fwd", "linear_dx", "lora_xa", "lora_da", "lora_wgr
 def lora_job(inp: torch.Tensor, w: torch.Tensor, out: torch.Tensor, scale: float = 1.0,
              transpose_out: bool = False) -> NF4LoraJob:
     """One job of the multi LoRA launches: `inp` [M, cols] (any row stride), `w` the small
-    operand, `out` the result; the tensors stay alive for the call (the caller keeps them)."""
+    operand, `out` the result.  Like make_lora's struct, the job holds references to its
+    tensors, so a temporary passed here stays allocated while the job lives."""
     _check_device(inp, w, out)
-    return NF4LoraJob(in_=inp.data_ptr(), ld=inp.stride(0), cols=inp.shape[1], w=w.data_ptr(),
-                      out=out.data_ptr(), scale=float(scale), transpose_out=int(transpose_out))
+    job = NF4LoraJob(in_=inp.data_ptr(), ld=inp.stride(0), cols=inp.shape[1], w=w.data_ptr(),
+                     out=out.data_ptr(), scale=float(scale), transpose_out=int(transpose_out))
+    job._tensors = (inp, w, out)
+    return job
 
 
 def _jobs(jobs):

@@ -95,7 +95,7 @@ def test_kernels_refuse_cpu_tensors_loudly():
         NF4Linear.apply(x, packed.view(-1), qs, None)
 
 
-def test_lora_struct_keeps_its_tensors_alive():
+def test_lora_struct_keeps_its_tensors_alive(monkeypatch):
     """make_lora stores raw pointers; a temporary passed to it (t=lora_xa(...)) must not return
     to torch's cache while the struct is in use, or the call's own output may be allocated over
     it.  The struct holds references: the tensor outlives the caller's last name for it."""
@@ -111,6 +111,18 @@ def test_lora_struct_keeps_its_tensors_alive():
     gc.collect()
     assert ref() is not None and lo.t == ref().data_ptr()
     del lo
+    gc.collect()
+    assert ref() is None
+    # the multi-launch LoRA jobs too (their device check switched off for CPU tensors)
+    monkeypatch.setattr(kernels, "_check_device", lambda *t: None)
+    out = torch.empty(4, 16, dtype=torch.float16)
+    ref = weakref.ref(out)
+    job = kernels.lora_job(torch.empty(4, 32, dtype=torch.float16),
+                           torch.empty(16, 32, dtype=torch.float16), out)
+    del out
+    gc.collect()
+    assert ref() is not None and job.out == ref().data_ptr()
+    del job
     gc.collect()
     assert ref() is None
 
